@@ -1,0 +1,394 @@
+/* q4_oracle.c -- CPU restatement of the reference's quantized routed-expert
+ * path.  TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg load it as the checker.  The product library
+ * (suzuku-engine-q4_amd/) never links, calls or falls back to it.
+ *
+ * Plain scalar C, no intrinsics, written from the reference's algorithm:
+ *
+ *   or_f16_to_f32        src/q4_quant.c:21-45
+ *   or_quant8            cpx_quant8, src/q4_cpuexp.c:605-637
+ *   or_dequant_row       dequant_iq3_s src/q4_quant.c:384-422,
+ *                        dequant_q8_0  src/q4_quant.c:131-140
+ *   or_group_sums        the exact int32 inside dq8_iq3_s (src/q4_cpuexp.c:
+ *                        855-892) and dq8_q8_0 (:1076-1096), one per 32 values
+ *   or_dot8              dq8_iq3_s / dq8_q8_0 fp32 result, including the
+ *                        8-lane FMA accumulation and the cpx_hsum fold order
+ *                        (src/q4_cpuexp.c:39-46)
+ *   or_softmax_topk      q4_softmax + q4_topk(renorm) src/q4_quant.c:715-755
+ *   or_pack              host pack, src/q4_moe.c:3404-3451 and bounds
+ *                        :3558-3571
+ *   or_moe_tokens        q4_cpuex_dispatch2 / _win job semantics
+ *                        (src/q4_cpuexp.c:2239-2321, :2387-2410, :2503-2753);
+ *                        also the MMQ prefill composition q4_moe.c:3697-3748
+ *                        + reduce_expert_k q4_rocm.cu:15739-15750 (same math)
+ *
+ * Pinning (see tests/test_oracle_*.py): or_quant8 and or_dot8 are compared
+ * bit-for-bit with the reference kernels compiled from source (oracle/_ref);
+ * or_group_sums against a brute-force integer dot over or_dequant_row;
+ * or_dequant_row against the reference's closed-form known answer
+ * (src/q4_test.c:51-57) and golden vectors; routing/pack against the
+ * reference's q4_softmax/q4_topk and the partition invariants of
+ * src/q4_test.c:2036-2081.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../include/q4mi_iq3s_grid.h"
+
+#define OR_T_Q8_0 8u
+#define OR_T_IQ3_S 21u
+
+float or_f16_to_f32(uint16_t h) {
+    uint32_t s = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t u;
+    if (e == 0) {
+        if (m == 0) {
+            u = s;
+        } else {
+            /* subnormal: normalise the mantissa */
+            int ex = 113;
+            while (!(m & 0x400u)) {
+                m <<= 1;
+                ex--;
+            }
+            u = s | ((uint32_t)ex << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        u = s | 0x7f800000u | (m << 13);
+    } else {
+        u = s | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint64_t or_row_bytes(uint32_t type, uint64_t n) {
+    if (type == OR_T_IQ3_S) return n % 256 ? 0 : n / 256 * 110;
+    if (type == OR_T_Q8_0) return n % 32 ? 0 : n / 32 * 34;
+    return 0;
+}
+
+/* _mm256_cvtps_epi32 under the default MXCSR: round to nearest even; a value
+ * that does not fit int32 (or NaN) becomes INT32_MIN.  The packs that follow
+ * saturate to int8. */
+static int8_t or_cvt_sat8(float v) {
+    if (!(v >= -2147483648.0f && v < 2147483648.0f)) return -128;
+    float r = nearbyintf(v);
+    if (r > 127.f) return 127;
+    if (r < -128.f) return -128;
+    return (int8_t)(int)r;
+}
+
+/* Per 32 values: a = max|x|; d = a/127; q = RNE(x * (a > 0 ? 127/a : 0));
+ * bs = sum(q). */
+void or_quant8(const float *x, uint64_t n, int8_t *q, float *d, int32_t *bs) {
+    for (uint64_t g = 0; g < n / 32; g++) {
+        const float *xb = x + 32 * g;
+        float a = 0.f;
+        for (int i = 0; i < 32; i++) {
+            float v = fabsf(xb[i]);
+            if (v > a) a = v;
+        }
+        d[g] = a / 127.f;
+        const float sc = a > 0.f ? 127.f / a : 0.f;
+        int32_t s = 0;
+        for (int i = 0; i < 32; i++) {
+            int8_t c = or_cvt_sat8(xb[i] * sc);
+            q[32 * g + i] = c;
+            s += c;
+        }
+        bs[g] = s;
+    }
+}
+
+/* Float dequantization, in the reference's element order. */
+int or_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *y) {
+    if (type == OR_T_Q8_0) {
+        for (uint64_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = w + 34 * b;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            const float d = or_f16_to_f32(dh);
+            for (int j = 0; j < 32; j++)
+                y[32 * b + j] = (float)(int8_t)blk[2 + j] * d;
+        }
+        return 1;
+    }
+    if (type != OR_T_IQ3_S || n % 256) return 0;
+    for (uint64_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = w + 110 * b;
+        uint16_t dh;
+        memcpy(&dh, blk, 2);
+        const float d = or_f16_to_f32(dh);
+        float *o = y + 256 * b;
+        /* 8 groups of 32: qs 8 bytes, one qh byte, 4 sign bytes, a nibble
+         * of scales[g/2] each. */
+        for (int g = 0; g < 8; g++) {
+            const uint8_t *qs = blk + 2 + 8 * g;
+            const uint8_t qh = blk[66 + g];
+            const uint8_t *sg = blk + 74 + 4 * g;
+            const int nib = (g & 1) ? blk[106 + g / 2] >> 4 : blk[106 + g / 2] & 15;
+            const float db = d * (1.f + 2.f * (float)nib);
+            for (int k = 0; k < 8; k++) {
+                const uint32_t idx = qs[k] | (((qh >> k) & 1u) << 8);
+                const uint32_t e = q4mi_iq3s_entry(idx);
+                for (int j = 0; j < 4; j++) {
+                    const int v = 4 * k + j; /* value index inside the group */
+                    const int neg = (sg[v / 8] >> (v % 8)) & 1;
+                    o[32 * g + v] =
+                        db * (float)((e >> (8 * j)) & 0xff) * (neg ? -1.f : 1.f);
+                }
+            }
+        }
+    }
+    return 1;
+}
+
+/* Signed integer weights of one 32-group and its integer multiplier:
+ * IQ3_S: w = +-grid byte, mult = 2s+1; Q8_0: w = int8, mult = 1. */
+static void or_group_ints(uint32_t type, const uint8_t *w, uint64_t g,
+                          int32_t wi[32], int32_t *mult) {
+    if (type == OR_T_Q8_0) {
+        const uint8_t *blk = w + 34 * g;
+        for (int j = 0; j < 32; j++) wi[j] = (int8_t)blk[2 + j];
+        *mult = 1;
+        return;
+    }
+    const uint8_t *blk = w + 110 * (g / 8);
+    const int j = (int)(g % 8);
+    const uint8_t *qs = blk + 2 + 8 * j;
+    const uint32_t h = blk[66 + j];
+    const uint32_t sg = (uint32_t)blk[74 + 4 * j] | ((uint32_t)blk[75 + 4 * j] << 8) |
+                        ((uint32_t)blk[76 + 4 * j] << 16) |
+                        ((uint32_t)blk[77 + 4 * j] << 24);
+    const uint8_t s = blk[106 + j / 2];
+    *mult = 2 * ((j & 1) ? (s >> 4) : (s & 15)) + 1;
+    for (int k = 0; k < 8; k++) {
+        const uint32_t e = q4mi_iq3s_entry(qs[k] | (((h >> k) & 1u) << 8));
+        for (int b = 0; b < 4; b++) {
+            const int v = 4 * k + b;
+            const int mag = (int)((e >> (8 * b)) & 0xff);
+            wi[v] = ((sg >> v) & 1u) ? -mag : mag;
+        }
+    }
+}
+
+/* Exact per-group sums S_g = mult_g * sum_i w_i q_i (int32). */
+int or_group_sums(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
+                  int32_t *s) {
+    if (!or_row_bytes(type, n)) return 0;
+    int32_t wi[32], mult;
+    for (uint64_t g = 0; g < n / 32; g++) {
+        or_group_ints(type, w, g, wi, &mult);
+        int32_t acc = 0;
+        for (int i = 0; i < 32; i++) acc += wi[i] * (int32_t)q[32 * g + i];
+        s[g] = acc * mult;
+    }
+    return 1;
+}
+
+/* fp32 row dot with the oracle's accumulation structure: lane l (0..7) of an
+ * 8-wide fp32 accumulator receives, per 32-group, fma(d_w*d_x, lane_int, acc)
+ * where lane_int = mult * sum of products of values 4l..4l+3; the result is
+ * the cpx_hsum fold ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). */
+float or_dot8(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
+              const float *dx) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t wi[32], mult;
+    for (uint64_t g = 0; g < n / 32; g++) {
+        or_group_ints(type, w, g, wi, &mult);
+        uint16_t dh;
+        if (type == OR_T_Q8_0)
+            memcpy(&dh, w + 34 * g, 2);
+        else
+            memcpy(&dh, w + 110 * (g / 8), 2);
+        const float dd = or_f16_to_f32(dh) * dx[g];
+        for (int l = 0; l < 8; l++) {
+            int32_t li = 0;
+            for (int b = 0; b < 4; b++) li += wi[4 * l + b] * (int32_t)q[32 * g + 4 * l + b];
+            acc[l] = fmaf(dd, (float)(li * mult), acc[l]);
+        }
+    }
+    const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+    const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+    return (l0 + l2) + (l1 + l3);
+}
+
+/* y[t*rows + r] = dot of row r with q8(x[t]), nt tokens. */
+int or_dot8_rows(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t n,
+                 const float *x, uint32_t nt, float *y) {
+    const uint64_t rb = or_row_bytes(type, n);
+    if (!rb) return 0;
+    int8_t *q = (int8_t *)malloc(n);
+    float *d = (float *)malloc(n / 32 * sizeof(float));
+    int32_t *bs = (int32_t *)malloc(n / 32 * sizeof(int32_t));
+    if (!q || !d || !bs) return 0;
+    for (uint32_t t = 0; t < nt; t++) {
+        or_quant8(x + (uint64_t)t * n, n, q, d, bs);
+        for (uint64_t r = 0; r < rows; r++)
+            y[(uint64_t)t * rows + r] = or_dot8(type, w + r * rb, n, q, d);
+    }
+    free(q);
+    free(d);
+    free(bs);
+    return 1;
+}
+
+/* q4_softmax (serial sum, index order) then q4_topk with renormalisation:
+ * strict '>' so that the earlier index wins ties. */
+void or_softmax_topk(const float *logits, uint32_t n, uint32_t k, int32_t *ids,
+                     float *wts) {
+    float *p = (float *)malloc(n * sizeof(float));
+    float m = logits[0];
+    for (uint32_t i = 1; i < n; i++)
+        if (logits[i] > m) m = logits[i];
+    float s = 0.f;
+    for (uint32_t i = 0; i < n; i++) {
+        p[i] = expf(logits[i] - m);
+        s += p[i];
+    }
+    const float inv = s > 0 ? 1.0f / s : 0.f;
+    for (uint32_t i = 0; i < n; i++) p[i] *= inv;
+    if (k > n) k = n;
+    for (uint32_t i = 0; i < k; i++) {
+        ids[i] = -1;
+        wts[i] = -INFINITY;
+    }
+    for (uint32_t i = 0; i < n; i++) {
+        const float v = p[i];
+        uint32_t pos = k;
+        while (pos > 0 && (ids[pos - 1] < 0 || v > wts[pos - 1])) pos--;
+        if (pos == k) continue;
+        for (uint32_t j = k - 1; j > pos; j--) {
+            ids[j] = ids[j - 1];
+            wts[j] = wts[j - 1];
+        }
+        ids[pos] = (int32_t)i;
+        wts[pos] = v;
+    }
+    float t = 0.f;
+    for (uint32_t i = 0; i < k; i++) t += wts[i];
+    if (t > 0) {
+        const float iv = 1.0f / t;
+        for (uint32_t i = 0; i < k; i++) wts[i] *= iv;
+    }
+    free(p);
+}
+
+/* Host stable pack per token group of gsz tokens.  Outputs:
+ *   ek[g*512+e]   rows of expert e in group g
+ *   a_tok[g*gsz*topk + p] token of packed row p (group-local p)
+ *   rsrc[t*topk+k] packed row of pick (t,k) (-1 for invalid ids), rw weight
+ *   stg[g*512+i], stgn[g]  used experts ascending
+ *   bounds[g*(n_exp+1) + e] = exclusive prefix, bounds[.. + n_exp] = rows */
+void or_pack(const int32_t *ids, const float *wts, uint32_t n_tok,
+             uint32_t topk, uint32_t n_exp, uint32_t gsz, int32_t *a_tok,
+             int32_t *rsrc, float *rw, uint32_t *ek, int32_t *stg,
+             uint32_t *stgn, int32_t *bounds) {
+    const uint32_t n_g = (n_tok + gsz - 1) / gsz;
+    uint32_t *cur = (uint32_t *)calloc((size_t)n_g * 512, sizeof(uint32_t));
+    memset(ek, 0, (size_t)n_g * 512 * sizeof(uint32_t));
+    memset(stgn, 0, n_g * sizeof(uint32_t));
+    for (uint32_t t = 0; t < n_tok; t++)
+        for (uint32_t k = 0; k < topk; k++) {
+            const int32_t e = ids[t * topk + k];
+            if (e >= 0 && e < (int32_t)n_exp) ek[(t / gsz) * 512 + e]++;
+        }
+    for (uint32_t g = 0; g < n_g; g++) {
+        uint32_t b = 0;
+        for (uint32_t e = 0; e < n_exp; e++) {
+            cur[g * 512 + e] = b;
+            bounds[g * (n_exp + 1) + e] = (int32_t)b;
+            b += ek[g * 512 + e];
+        }
+        bounds[g * (n_exp + 1) + n_exp] = (int32_t)b;
+    }
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const uint32_t g = t / gsz, seg = g * gsz * topk;
+        for (uint32_t k = 0; k < topk; k++) {
+            const int32_t e = ids[t * topk + k];
+            if (e < 0 || e >= (int32_t)n_exp) {
+                rsrc[t * topk + k] = -1;
+                rw[t * topk + k] = 0.f;
+                continue;
+            }
+            const uint32_t p = cur[g * 512 + e]++;
+            a_tok[seg + p] = (int32_t)t;
+            rsrc[t * topk + k] = (int32_t)p;
+            rw[t * topk + k] = wts[t * topk + k];
+        }
+    }
+    for (uint32_t g = 0; g < n_g; g++)
+        for (uint32_t e = 0; e < n_exp; e++)
+            if (ek[g * 512 + e]) stg[g * 512 + stgn[g]++] = (int32_t)e;
+    free(cur);
+}
+
+static float or_silu(float v) { return v / (1.f + expf(-v)); }
+
+/* Routed-expert FFN over T tokens, the CPU expert job's arithmetic.
+ * Experts live at base + id*stride as gate[n_ff][n_embd] | up | down
+ * [n_embd][n_ff] (src/q4_expert.c:962-982).  Per token t and pick j
+ * (expert ids[t*k+j], weight wts[t*k+j]):
+ *   xq = q8(x[t]); h_r = silu(gate_r . xq) * (up_r . xq); hq = q8(h);
+ *   pd_r = down_r . hq
+ * mode 0 (decode job): y[t][r] accumulates wts*pd_r in pick order, starting
+ *   from zero (the reference's CAS adds land in a nondeterministic order).
+ * mode 1 (prefill reduce): y[t][r] += sum_j wts*pd_r (sum formed first, in
+ *   pick order), as reduce_expert_k does.
+ * h_out (optional) receives h for each (t, j): [T*k][n_ff]. */
+int or_moe_tokens(uint32_t n_embd, uint32_t n_ff, uint32_t t_gu, uint32_t t_d,
+                  const uint8_t *base, uint64_t stride, const float *x,
+                  uint32_t T, const int32_t *ids, const float *wts, uint32_t k,
+                  float *y, int mode, float *h_out) {
+    const uint64_t rg = or_row_bytes(t_gu, n_embd), rd = or_row_bytes(t_d, n_ff);
+    if (!rg || !rd) return 0;
+    int8_t *xq = (int8_t *)malloc(n_embd);
+    float *xd = (float *)malloc(n_embd / 32 * sizeof(float));
+    int32_t *bs = (int32_t *)malloc((n_embd / 32 + n_ff / 32) * sizeof(int32_t));
+    float *h = (float *)malloc(n_ff * sizeof(float));
+    int8_t *hq = (int8_t *)malloc(n_ff);
+    float *hd = (float *)malloc(n_ff / 32 * sizeof(float));
+    float *acc = (float *)malloc(n_embd * sizeof(float));
+    for (uint32_t t = 0; t < T; t++) {
+        or_quant8(x + (uint64_t)t * n_embd, n_embd, xq, xd, bs);
+        float *yt = y + (uint64_t)t * n_embd;
+        if (mode == 0) memset(yt, 0, n_embd * sizeof(float));
+        else memset(acc, 0, n_embd * sizeof(float));
+        for (uint32_t j = 0; j < k; j++) {
+            const int32_t e = ids[t * k + j];
+            if (e < 0) continue;
+            const float wt = wts[t * k + j];
+            const uint8_t *pe = base + (uint64_t)e * stride;
+            const uint8_t *wg = pe, *wu = pe + (uint64_t)n_ff * rg;
+            const uint8_t *wd = pe + 2ull * n_ff * rg;
+            for (uint32_t r = 0; r < n_ff; r++) {
+                const float gv = or_dot8(t_gu, wg + r * rg, n_embd, xq, xd);
+                const float uv = or_dot8(t_gu, wu + r * rg, n_embd, xq, xd);
+                h[r] = or_silu(gv) * uv;
+            }
+            if (h_out) memcpy(h_out + ((uint64_t)t * k + j) * n_ff, h, n_ff * sizeof(float));
+            or_quant8(h, n_ff, hq, hd, bs);
+            for (uint32_t r = 0; r < n_embd; r++) {
+                const float dv = or_dot8(t_d, wd + r * rd, n_ff, hq, hd);
+                if (mode == 0) yt[r] += wt * dv;
+                else acc[r] += wt * dv;
+            }
+        }
+        if (mode != 0)
+            for (uint32_t r = 0; r < n_embd; r++) yt[r] += acc[r];
+    }
+    free(xq);
+    free(xd);
+    free(bs);
+    free(h);
+    free(hq);
+    free(hd);
+    free(acc);
+    return 1;
+}

@@ -1,0 +1,171 @@
+// Dense decode MMVQ: y[t][r] = scale * (W_r . q8(x_t)) for 1..8 tokens over
+// IQ3_S or Q8_0 weight rows.  C ABI: q4_mmvq_n and friends (reference
+// src/q4_mmvq.cu:266-349, src/q4.h:914-927) plus q4mi_mmvq, which takes
+// already-quantized activations and can export the per-group int32 sums.
+#include <stdlib.h>
+
+#include "mmvq_engine.h"
+#include "q4mi_internal.h"
+
+namespace q4mi {
+
+bool quant8_launch(const float *x, const int32_t *ids, uint64_t rows, uint32_t cols,
+                   int8_t *q, float *d, int32_t *bs);
+
+template <class F, int NT, int TPR, int GPT>
+__global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uint32_t rows,
+                                              uint32_t K, uint32_t rb, uint32_t R,
+                                              const int8_t *__restrict__ xq,
+                                              const float *__restrict__ xd, uint32_t nt,
+                                              float *__restrict__ y, float scale,
+                                              int32_t *__restrict__ sums) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    Iq3sLds *tab = (Iq3sLds *)smem;
+    uint8_t *tile = smem + (F::kTables ? sizeof(Iq3sLds) : 0);
+    const uint32_t tid = threadIdx.x;
+    const uint32_t r0 = blockIdx.x * R;
+    const uint32_t nr = min(R, rows - r0);
+    if (F::kTables) q4mi_iq3s_tables_init(tab, tid, 256);
+    stage_tile(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
+    const uint32_t gi = tid % TPR;
+    XRegs<NT, GPT> x;
+    load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
+    __syncthreads();
+    const uint32_t G = K / 32;
+    for (uint32_t rr = tid / TPR; rr < nr; rr += 256 / TPR) {
+        float acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t] = 0.f;
+        int32_t *srow = sums ? sums + (size_t)(r0 + rr) * G : nullptr;
+        row_dot<F, NT, GPT, TPR>(tab, tile, (const uint32_t *)tile, rr * rb, gi, x, acc, srow,
+                                 (size_t)rows * G);
+        reduce_acc<TPR, NT>(acc);
+        if (gi == 0) {
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                if ((uint32_t)t < nt) y[(size_t)t * rows + r0 + rr] = scale * acc[t];
+        }
+    }
+}
+
+template <class F, int NT>
+static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const int8_t *xq,
+                           const float *xd, uint32_t nt, float *y, float scale,
+                           int32_t *sums) {
+    const uint32_t G = K / 32;
+    const RowLayout L = layout_for(G);
+    const uint32_t rb = (uint32_t)q4mi_row_bytes(F::kType, K);
+    const uint32_t target = F::kType == Q4MI_T_Q8_0 ? 24576u : 14336u;
+    const uint32_t R = tile_rows(rb, L.tpr, target);
+    const size_t lds = (F::kTables ? sizeof(Iq3sLds) : 0) + (size_t)R * rb + 64;
+    const dim3 grid((rows + R - 1) / R), blk(256);
+#define Q4MI_L(T, P)                                                                     \
+    if (L.tpr == T && L.gpt == P) {                                                      \
+        mmvq_k<F, NT, T, P><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xq, xd, nt, \
+                                                          y, scale, sums);               \
+        return launch_ok("mmvq_k");                                                      \
+    }
+    Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+#undef Q4MI_L
+    set_error("mmvq: K=%u not covered", K);
+    return false;
+}
+
+template <class F>
+static bool mmvq_launch(const uint8_t *W, uint32_t rows, uint32_t K, const int8_t *xq,
+                        const float *xd, uint32_t nt, float *y, float scale, int32_t *sums) {
+    if (nt == 1) return mmvq_launch_nt<F, 1>(W, rows, K, xq, xd, nt, y, scale, sums);
+    if (nt == 2) return mmvq_launch_nt<F, 2>(W, rows, K, xq, xd, nt, y, scale, sums);
+    if (nt <= 4) return mmvq_launch_nt<F, 4>(W, rows, K, xq, xd, nt, y, scale, sums);
+    return mmvq_launch_nt<F, 8>(W, rows, K, xq, xd, nt, y, scale, sums);
+}
+
+bool mmvq_covered(uint32_t ty, uint64_t K) {
+    if (ty != Q4MI_T_IQ3_S && ty != Q4MI_T_Q8_0) return false;
+    if (!q4mi_row_bytes(ty, K) || K > 8192) return false;
+    return layout_for((uint32_t)(K / 32)).tpr != 0;
+}
+
+bool mmvq_q8(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const int8_t *xq,
+             const float *xd, uint32_t nt, float *y, float scale, int32_t *sums) {
+    if (ty == Q4MI_T_IQ3_S)
+        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, xq, xd, nt, y, scale, sums);
+    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, xq, xd, nt, y, scale, sums);
+}
+
+static int g_on = -1;
+static const float *g_hold = nullptr;
+static const float *g_cur_x = nullptr;
+static uint64_t g_cur_k = 0;
+static uint32_t g_cur_n = 0;
+
+}  // namespace q4mi
+
+using namespace q4mi;
+
+extern "C" {
+
+/* Q4_MMVQ=0 turns the int8 GEMV off (callers keep another path); any
+ * other value or unset: on. */
+int q4_mmvq_on(void) {
+    if (g_on < 0) {
+        const char *e = getenv("Q4_MMVQ");
+        g_on = (e && e[0] == '0') ? 0 : 1;
+    }
+    return g_on;
+}
+void q4_mmvq_set(int v) { g_on = v; }
+/* Kept for ABI shape: this library has no verify-only policy. */
+void q4_mmvq_verify(int on) { (void)on; }
+
+/* Allocate the activation buffers (call outside any stream capture). */
+void q4_mmvq_warm(void) { (void)ensure_xq((size_t)8 * 8192); }
+
+void q4_mmvq_hold(const float *d_x) {
+    g_hold = d_x;
+    g_cur_x = nullptr;
+}
+void q4_mmvq_release(void) {
+    g_hold = nullptr;
+    g_cur_x = nullptr;
+}
+
+/* y[t*nrows + r] = scale * dot(W row r, q8(x[t])), t < n (1..8).  Types:
+ * IQ3_S, Q8_0; ncols a multiple of 256 (IQ3_S) / 32 (Q8_0) with
+ * ncols/32 in {8,16,32,64,128,256}.  false = not covered; nothing launched. */
+bool q4_mmvq_n(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
+               const float *d_x, float *d_y, float scale, uint32_t n) {
+    if (!q4_mmvq_on() || n < 1 || n > 8 || !d_w || !d_x || !d_y || !nrows ||
+        nrows > 0x7fffffffu || !mmvq_covered(ty, ncols)) {
+        set_error("q4_mmvq_n: not covered");
+        return false;
+    }
+    if (!ensure_xq((size_t)8 * 8192)) return false;
+    Scratch &s = scratch();
+    const bool reuse = g_hold && g_hold == d_x && g_cur_x == d_x && g_cur_k == ncols &&
+                       g_cur_n >= n;
+    if (!reuse) {
+        if (!quant8_launch(d_x, nullptr, n, (uint32_t)ncols, s.xq, s.xd, nullptr))
+            return false;
+        g_cur_x = d_x;
+        g_cur_k = ncols;
+        g_cur_n = n;
+    }
+    return mmvq_q8(ty, d_w, nrows, ncols, s.xq, s.xd, n, d_y, scale, nullptr);
+}
+
+/* Pre-quantized variant: xq [n][ncols] int8, xd [n][ncols/32] fp32 (the
+ * q4mi_quant8 layout).  d_sums (optional) receives the exact int32 group
+ * sums, d_sums[(t*nrows + r)*(ncols/32) + g] = (2s+1) * sum w*q. */
+bool q4mi_mmvq(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
+               const int8_t *d_xq, const float *d_xd, uint32_t n, float *d_y, float scale,
+               int32_t *d_sums) {
+    if (n < 1 || n > 8 || !d_w || !d_xq || !d_xd || !d_y || !nrows || nrows > 0x7fffffffu ||
+        !mmvq_covered(ty, ncols) || ((uintptr_t)d_xq & 15)) {
+        set_error("q4mi_mmvq: not covered");
+        return false;
+    }
+    return mmvq_q8(ty, d_w, nrows, ncols, d_xq, d_xd, n, d_y, scale, d_sums);
+}
+
+}  // extern "C"

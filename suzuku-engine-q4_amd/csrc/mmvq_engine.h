@@ -1,0 +1,149 @@
+// Int8-activation row-dot engine for decode (MMVQ), wave64 / gfx950.
+//
+// A 256-thread block stages a tile of weight rows into LDS with coalesced
+// 16-byte loads (IQ3_S rows are 110-byte superblocks, not 16-byte aligned
+// units, so they are decoded from LDS, never straight from global memory).
+// TPR lanes cooperate on one row; lane gi owns the row's 32-value groups
+// gi, gi+TPR, ... (GPT of them), so its q8 activations for those groups stay
+// in registers for every row of the tile.  Per group the lane decodes the
+// weights to signed int8 quads, takes v_dot4_i32_i8 against the activation
+// quads, scales the exact int32 group sum by (2s+1) and accumulates
+// float(S) * (d_w * d_x).  A shuffle reduction over the TPR lanes finishes
+// the row.
+#pragma once
+#include "q4mi_common.h"
+
+namespace q4mi {
+
+struct FmtIQ3S {
+    static constexpr uint32_t kType = Q4MI_T_IQ3_S;
+    static constexpr bool kTables = true;
+    __device__ static inline void decode(const Iq3sLds *tab, const uint8_t *lb,
+                                         const uint32_t *lw, uint32_t row, uint32_t g,
+                                         Iq3sGroup &o) {
+        q4mi_iq3s_decode(tab, lb, lw, row, g, o);
+    }
+};
+
+struct FmtQ80 {
+    static constexpr uint32_t kType = Q4MI_T_Q8_0;
+    static constexpr bool kTables = false;
+    __device__ static inline void decode(const Iq3sLds *, const uint8_t *lb,
+                                         const uint32_t *lw, uint32_t row, uint32_t g,
+                                         Iq3sGroup &o) {
+        const uint32_t B = row + g * Q80_BYTES;
+        o.d = q4mi_h2f(lds_u16_at(lb, B));
+        o.mult = 1;
+        const uint32_t i0 = (B + 2u) >> 2, sh = (B + 2u) & 3u;
+        uint32_t prev = lw[i0];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t nx = lw[i0 + 1 + k];
+            o.w[k] = (int32_t)__builtin_amdgcn_alignbyte(nx, prev, sh);
+            prev = nx;
+        }
+    }
+};
+
+// q8 activations of this lane's GPT groups for NT tokens.
+template <int NT, int GPT>
+struct XRegs {
+    int32_t q[GPT][NT][8];
+    float d[GPT][NT];
+};
+
+// xq: [nt][K] int8, xd: [nt][K/32] (global or LDS); tokens >= nt read as 0.
+template <int NT, int GPT, int TPR>
+__device__ inline void load_xregs(XRegs<NT, GPT> &x, const int8_t *xq, const float *xd,
+                                  uint32_t K, uint32_t nt, uint32_t gi) {
+#pragma unroll
+    for (int m = 0; m < GPT; m++) {
+        const uint32_t g = gi + TPR * m;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if ((uint32_t)t < nt) {
+                const int4 a = *(const int4 *)(xq + (size_t)t * K + 32u * g);
+                const int4 b = *(const int4 *)(xq + (size_t)t * K + 32u * g + 16u);
+                x.q[m][t][0] = a.x; x.q[m][t][1] = a.y; x.q[m][t][2] = a.z; x.q[m][t][3] = a.w;
+                x.q[m][t][4] = b.x; x.q[m][t][5] = b.y; x.q[m][t][6] = b.z; x.q[m][t][7] = b.w;
+                x.d[m][t] = xd[(size_t)t * (K / 32) + g];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; k++) x.q[m][t][k] = 0;
+                x.d[m][t] = 0.f;
+            }
+        }
+    }
+}
+
+// Partial dot of one row (this lane's groups) for NT tokens, added to acc.
+// sums (optional): per-token int32 group sums, sums[t * sum_tstride + g].
+template <class F, int NT, int GPT, int TPR>
+__device__ inline void row_dot(const Iq3sLds *tab, const uint8_t *lb, const uint32_t *lw,
+                               uint32_t row, uint32_t gi, const XRegs<NT, GPT> &x,
+                               float (&acc)[NT], int32_t *sums, size_t sum_tstride) {
+#pragma unroll
+    for (int m = 0; m < GPT; m++) {
+        const uint32_t g = gi + TPR * m;
+        Iq3sGroup w;
+        F::decode(tab, lb, lw, row, g, w);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            int s = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) s = q4mi_sdot4(w.w[k], x.q[m][t][k], s);
+            s *= w.mult;
+            acc[t] = fmaf((float)s, w.d * x.d[m][t], acc[t]);
+            if (sums) sums[(size_t)t * sum_tstride + g] = s;
+        }
+    }
+}
+
+// Copy nbytes (even) from global src to LDS dst with the widest aligned
+// accesses the addresses allow; all threads of the block take part.
+__device__ inline void stage_tile(uint8_t *dst, const uint8_t *src, uint32_t nbytes,
+                                  uint32_t tid, uint32_t nthr) {
+    const uintptr_t a = (uintptr_t)src | nbytes;
+    if ((a & 15u) == 0) {
+        const uint4 *s = (const uint4 *)src;
+        uint4 *d = (uint4 *)dst;
+        for (uint32_t i = tid; i < nbytes / 16; i += nthr) d[i] = s[i];
+    } else if ((a & 3u) == 0) {
+        const uint32_t *s = (const uint32_t *)src;
+        uint32_t *d = (uint32_t *)dst;
+        for (uint32_t i = tid; i < nbytes / 4; i += nthr) d[i] = s[i];
+    } else {
+        const uint16_t *s = (const uint16_t *)src;
+        uint16_t *d = (uint16_t *)dst;
+        for (uint32_t i = tid; i < nbytes / 2; i += nthr) d[i] = s[i];
+    }
+}
+
+template <int TPR, int NT>
+__device__ inline void reduce_acc(float (&acc)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = q4mi_sum_width<TPR>(acc[t]);
+}
+
+// Layout of lanes over a row of G = K/32 groups.
+struct RowLayout {
+    int tpr, gpt;
+};
+inline RowLayout layout_for(uint32_t G) {
+    if (G == 8 || G == 16 || G == 32 || G == 64) return {(int)G, 1};
+    if (G == 128) return {64, 2};
+    if (G == 256) return {64, 4};
+    return {0, 0};
+}
+
+// Rows per block so that a tile is about `target` bytes, a multiple of the
+// rows one pass covers (256 / tpr).
+inline uint32_t tile_rows(uint32_t rb, int tpr, uint32_t target) {
+    const uint32_t rpp = 256u / (uint32_t)tpr;
+    uint32_t r = target / rb;
+    r = r / rpp * rpp;
+    if (r < rpp) r = rpp;
+    return r;
+}
+
+}  // namespace q4mi

@@ -1,0 +1,41 @@
+// Host-side shared state of the library (one process, one device).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace q4mi {
+
+// Stream every entry point launches on (q4_hip_stream / q4mi_set_stream).
+hipStream_t stream();
+
+// Library-owned device scratch, grown on demand.  Growing allocates, so it is
+// illegal inside a graph capture; q4_hip_moe_scratch_warm / q4_mmvq_warm
+// size everything up front.
+struct Scratch {
+    float *pd = nullptr;        // MoE decode partials [64][8][n_embd]
+    size_t pd_floats = 0;
+    uint32_t *tickets = nullptr;  // per-row-tile completion counters
+    size_t n_tickets = 0;
+    int8_t *xq = nullptr;       // q8 activations for q4_mmvq_n
+    float *xd = nullptr;
+    size_t xq_elems = 0;
+};
+Scratch &scratch();
+bool ensure_pd(size_t floats);
+bool ensure_tickets(size_t n);
+bool ensure_xq(size_t elems);
+
+// Error reporting: entry points return false; the last message is kept.
+void set_error(const char *fmt, ...);
+
+inline bool launch_ok(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+        return false;
+    }
+    return true;
+}
+
+}  // namespace q4mi

@@ -1,0 +1,110 @@
+"""Host-side mirror of the reference's routed-expert GPU entry points.
+
+The product is the C-ABI library lib/libq4mi.so (declared in
+include/q4mi.h).  This module binds it with ctypes so Python callers and the
+tests drive exactly the entry points a C host engine would link: the
+reference's q4.h names (q4_hip_moe_exec, q4_hip_moe_exec_win, q4_mmvq_n,
+q4_mmq_*, q4_hip_route_pf, q4_hip_assign_pf, q4_hip_expert_reduce, ...)
+plus this library's additions (q4mi_*).
+
+Arguments are device pointers (ints) or torch CUDA tensors; PyTorch supplies
+device memory and the stream, nothing else.  There is no CPU fallback: if the
+library is missing, importing `lib()` raises.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libq4mi.so")
+
+T_Q8_0 = 8
+T_IQ3_S = 21
+
+_c = ctypes
+_vp = _c.c_void_p
+_u32 = _c.c_uint32
+_u64 = _c.c_uint64
+_f32 = _c.c_float
+_b = _c.c_bool
+
+# name: (restype, argtypes)
+_SIGS = {
+    "q4_hip_stream": (_vp, []),
+    "q4mi_set_stream": (None, [_vp]),
+    "q4mi_last_error": (_c.c_char_p, []),
+    "q4mi_device_ok": (_c.c_int, []),
+    "q4mi_quant8": (_b, [_vp, _vp, _u64, _u64, _vp, _vp, _vp]),
+    "q4_mmvq_on": (_c.c_int, []),
+    "q4_mmvq_set": (None, [_c.c_int]),
+    "q4_mmvq_verify": (None, [_c.c_int]),
+    "q4_mmvq_warm": (None, []),
+    "q4_mmvq_hold": (None, [_vp]),
+    "q4_mmvq_release": (None, []),
+    "q4_mmvq_n": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _f32, _u32]),
+    "q4mi_mmvq": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _u32, _vp, _f32, _vp]),
+    "q4_hip_moe_scratch_warm": (None, []),
+    "q4_hip_moe_exec": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32, _u64,
+                             _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_moe_exec_dev": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u64, _u32, _u64, _u32, _u64,
+                                 _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_moe_win_ok": (_b, [_u32, _u32, _u32, _u32, _u32, _u32]),
+    "q4_hip_moe_exec_win": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
+                                 _u64, _vp, _vp, _vp, _u32, _u32, _u32]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises if it was not built: no silent fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("q4mi: %s is missing; build it with __graft_entry__.build()"
+                               % LIB_PATH)
+        L = _c.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name, None)
+            if f is None:
+                continue
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def ptr(t):
+    """Device pointer of a torch tensor (or an int / None)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def last_error():
+    e = lib().q4mi_last_error()
+    return e.decode() if e else ""
+
+
+def check(ok, what):
+    if not ok:
+        raise RuntimeError("%s failed: %s" % (what, last_error()))
+
+
+def use_torch_stream():
+    """Launch on torch's current stream (so torch ops and ours are ordered)."""
+    import torch
+    lib().q4mi_set_stream(_c.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def row_bytes(ty, n):
+    if ty == T_IQ3_S:
+        return n // 256 * 110
+    if ty == T_Q8_0:
+        return n // 32 * 34
+    raise ValueError(ty)

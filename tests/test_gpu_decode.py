@@ -1,0 +1,285 @@
+"""GPU parity: q8 quantizer, dense MMVQ (IQ3_S, Q8_0) and the routed-expert
+decode / verify window, through the C ABI, against the C oracle.
+
+Bars: q8 codes, d, code sums and int32 group sums bit-exact; fp32 outputs
+max relative error <= 1e-3 (|err| / max(|ref|, 1e-3 * max|ref|)).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+import oracle as om
+import q4mi
+from q4mi import synth
+
+pytestmark = pytest.mark.gpu
+T_IQ3_S, T_Q8_0 = q4mi.T_IQ3_S, q4mi.T_Q8_0
+TOL = 1e-3
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def empty(shape, dtype):
+    import torch
+    return torch.empty(shape, dtype=dtype, device="cuda")
+
+
+def quant_gpu(L, x, ids=None):
+    import torch
+    x = np.atleast_2d(x)
+    rows = x.shape[0] if ids is None else len(ids)
+    K = x.shape[1]
+    dx = dev(x)
+    di = dev(np.asarray(ids, np.int32)) if ids is not None else None
+    q = empty((rows, K), torch.int8)
+    d = empty((rows, K // 32), torch.float32)
+    bs = empty((rows, K // 32), torch.int32)
+    q4mi.check(L.q4mi_quant8(q4mi.ptr(dx), q4mi.ptr(di), rows, K, q4mi.ptr(q), q4mi.ptr(d),
+                             q4mi.ptr(bs)), "q4mi_quant8")
+    return host(q), host(d), host(bs)
+
+
+def test_quant8_bitexact(gpu, oracle):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((6, 4096)) * rng.choice([1e-4, 1, 50], (6, 4096))).astype(np.float32)
+    x[0, 0:32] = 0
+    x[1, 32:64] = np.arange(32) - 16.5
+    x[1, 63] = 127
+    x[2, 64:96] = 1e-30
+    q, d, bs = quant_gpu(gpu, x)
+    for r in range(6):
+        oq, od, obs = oracle.quant8(x[r])
+        assert np.array_equal(q[r], oq)
+        assert np.array_equal(d[r].view(np.uint32), od.view(np.uint32))
+        assert np.array_equal(bs[r], obs)
+    # gathered rows (the prefill quantizer's ids form)
+    ids = [5, 0, 5, 3]
+    q2, d2, _ = quant_gpu(gpu, x, ids)
+    for i, r in enumerate(ids):
+        assert np.array_equal(q2[i], q[r]) and np.array_equal(d2[i], d[r])
+
+
+def mmvq_gpu(L, ty, w, rows, K, x, sums=False):
+    import torch
+    x = np.atleast_2d(x).astype(np.float32)
+    nt = x.shape[0]
+    q, d, _ = quant_gpu(L, x)
+    dw, dq, dd = dev(w), dev(q), dev(d)
+    y = empty((nt, rows), torch.float32)
+    s = empty((nt, rows, K // 32), torch.int32) if sums else None
+    q4mi.check(L.q4mi_mmvq(ty, q4mi.ptr(dw), rows, K, q4mi.ptr(dq), q4mi.ptr(dd), nt,
+                           q4mi.ptr(y), 1.0, q4mi.ptr(s)), "q4mi_mmvq")
+    return host(y), (host(s) if sums else None)
+
+
+@pytest.mark.parametrize("ty,K,rows,nt", [(T_IQ3_S, 2048, 300, 1), (T_IQ3_S, 512, 200, 3),
+                                          (T_IQ3_S, 4096, 64, 2), (T_IQ3_S, 8192, 16, 1),
+                                          (T_Q8_0, 2048, 300, 1), (T_Q8_0, 512, 100, 4),
+                                          (T_Q8_0, 256, 40, 8)])
+def test_mmvq_sums_and_y(gpu, oracle, ty, K, rows, nt):
+    rng = np.random.default_rng(K + rows + nt)
+    w = synth.matrix(rng, ty, rows, K)
+    x = rng.standard_normal((nt, K)).astype(np.float32)
+    y, s = mmvq_gpu(gpu, ty, w, rows, K, x, sums=True)
+    rb = om.row_bytes(ty, K)
+    for t in range(nt):
+        q, d, _ = oracle.quant8(x[t])
+        for r in range(0, rows, 7):
+            os_ = oracle.group_sums(ty, w[r * rb:(r + 1) * rb], K, q)
+            assert np.array_equal(s[t, r], os_), (t, r)
+    yo = oracle.dot8_rows(ty, w, rows, K, x)
+    assert rel_err(y, yo) <= TOL
+
+
+def test_mmvq_batch_invariant(gpu):
+    """A row's result does not depend on how many tokens share the launch."""
+    rng = np.random.default_rng(12)
+    K, rows = 2048, 128
+    w = synth.matrix(rng, T_IQ3_S, rows, K)
+    x = rng.standard_normal((8, K)).astype(np.float32)
+    y8, _ = mmvq_gpu(gpu, T_IQ3_S, w, rows, K, x)
+    for nt in (1, 2, 3, 5):
+        yn, _ = mmvq_gpu(gpu, T_IQ3_S, w, rows, K, x[:nt])
+        assert np.array_equal(yn.view(np.uint32), y8[:nt].view(np.uint32))
+
+
+def test_q4_mmvq_n_abi(gpu, oracle):
+    """The reference's q4_mmvq_n entry: fp32 x in, y[t*rows+r] = scale*dot."""
+    import torch
+    rng = np.random.default_rng(13)
+    K, rows, n = 2048, 256, 4
+    w = synth.matrix(rng, T_Q8_0, rows, K)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    dw, dx = dev(w), dev(x)
+    y = empty((n, rows), torch.float32)
+    gpu.q4_mmvq_warm()
+    q4mi.check(gpu.q4_mmvq_n(T_Q8_0, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y), 0.5, n),
+               "q4_mmvq_n")
+    yo = oracle.dot8_rows(T_Q8_0, w, rows, K, x) * 0.5
+    assert rel_err(host(y), yo) <= TOL
+    # rejected shapes launch nothing and return false
+    assert not gpu.q4_mmvq_n(T_Q8_0, q4mi.ptr(dw), rows, 2000, q4mi.ptr(dx), q4mi.ptr(y), 1.0, n)
+    assert not gpu.q4_mmvq_n(T_Q8_0, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y), 1.0, 9)
+    assert not gpu.q4_mmvq_n(99, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y), 1.0, 1)
+
+
+def test_config0_full(gpu, oracle):
+    """IQ3_S 4096x4096, one token."""
+    rng = np.random.default_rng(0)
+    K = rows = 4096
+    w = synth.matrix(rng, T_IQ3_S, rows, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    y, s = mmvq_gpu(gpu, T_IQ3_S, w, rows, K, x, sums=True)
+    yo = oracle.dot8_rows(T_IQ3_S, w, rows, K, x)
+    assert rel_err(y, yo) <= TOL
+    q, _, _ = oracle.quant8(x)
+    rb = om.row_bytes(T_IQ3_S, K)
+    for r in rng.choice(rows, 64, replace=False):
+        assert np.array_equal(s[0, r], oracle.group_sums(T_IQ3_S, w[r * rb:(r + 1) * rb], K, q))
+
+
+# ------------------------------------------------------------ MoE decode
+
+class Layer:
+    """A MoE layer at BASELINE config shapes: 512 routed experts + 1 shared
+    (slot 512), hidden 2048, expert intermediate 512, all IQ3_S."""
+
+    def __init__(self, seed, n_exp=513, n_embd=2048, n_ff=512):
+        rng = np.random.default_rng(seed)
+        self.n_embd, self.n_ff, self.n_exp = n_embd, n_ff, n_exp
+        self.arena = synth.expert_arena(rng, n_exp, n_embd, n_ff)
+        self.stride, self.og, self.ou, self.od = synth.expert_stride(n_embd, n_ff)
+        self.rng = rng
+        self.d_arena = dev(self.arena)
+
+
+_LAYER = {}
+
+
+def layer():
+    if "l" not in _LAYER:
+        _LAYER["l"] = Layer(20)
+    return _LAYER["l"]
+
+
+def moe_exec_host(L, ly, x, ids, wts, y0=None):
+    import torch
+    dx = dev(x.astype(np.float32))
+    y = dev(np.zeros(ly.n_embd, np.float32) if y0 is None else y0)
+    ids = np.ascontiguousarray(ids, np.int32)
+    wts = np.ascontiguousarray(wts, np.float32)
+    ok = L.q4_hip_moe_exec(q4mi.ptr(ly.d_arena), ly.stride,
+                           ids.ctypes.data_as(ctypes.c_void_p), wts.ctypes.data_as(ctypes.c_void_p),
+                           len(ids), T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od,
+                           q4mi.ptr(dx), None, None, None, q4mi.ptr(y), ly.n_ff, ly.n_embd,
+                           ly.n_embd)
+    q4mi.check(ok, "q4_hip_moe_exec")
+    return host(y)
+
+
+def routed_ids(oracle, rng, k=10, E=512):
+    lg = rng.standard_normal((1, E)).astype(np.float32)
+    ids, wts = oracle.softmax_topk(lg, k)
+    return ids[0], wts[0]
+
+
+def test_moe_decode_config2(gpu, oracle):
+    """top-10 routed + shared expert (weight 1), 1 token."""
+    ly = layer()
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal(ly.n_embd).astype(np.float32)
+    ids, wts = routed_ids(oracle, rng)
+    ids = np.append(ids, 512).astype(np.int32)
+    wts = np.append(wts, 1.0).astype(np.float32)
+    y = moe_exec_host(gpu, ly, x, ids, wts)
+    yo = oracle.moe_tokens(ly.n_embd, ly.n_ff, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x,
+                           ids[None], wts[None])[0]
+    assert rel_err(y, yo) <= TOL
+    # accumulates into y, deterministically
+    y2 = moe_exec_host(gpu, ly, x, ids, wts, y0=y)
+    assert np.array_equal((y + y).view(np.uint32), y2.view(np.uint32)) or rel_err(y2, 2 * yo) <= TOL
+    y3 = moe_exec_host(gpu, ly, x, ids, wts)
+    assert np.array_equal(y.view(np.uint32), y3.view(np.uint32))
+
+
+def test_moe_exec_dev_and_rejects(gpu, oracle):
+    import torch
+    ly = layer()
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal(ly.n_embd).astype(np.float32)
+    ids, wts = routed_ids(oracle, rng, k=8)
+    es = np.full(64, -1, np.int32)
+    ew = np.zeros(64, np.float32)
+    es[:8], ew[:8] = ids, wts
+    d_es, d_ew, d_n = dev(es), dev(ew), dev(np.array([8], np.int32))
+    dx = dev(x)
+    y = dev(np.zeros(ly.n_embd, np.float32))
+    ok = gpu.q4_hip_moe_exec_dev(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es), q4mi.ptr(d_ew),
+                                 q4mi.ptr(d_n), T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od,
+                                 q4mi.ptr(dx), None, None, None, q4mi.ptr(y), ly.n_ff, ly.n_embd,
+                                 ly.n_embd)
+    q4mi.check(ok, "q4_hip_moe_exec_dev")
+    yo = oracle.moe_tokens(ly.n_embd, ly.n_ff, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x,
+                           ids[None], wts[None])[0]
+    assert rel_err(host(y), yo) <= TOL
+    # unsupported shapes/types are rejected before any launch (y untouched)
+    before = host(y).copy()
+    idh = np.ascontiguousarray(ids, np.int32)
+    wh = np.ascontiguousarray(wts, np.float32)
+    for gt, ut, dt, ff in ((T_IQ3_S, 2, T_IQ3_S, ly.n_ff), (T_IQ3_S, T_IQ3_S, 99, ly.n_ff),
+                           (T_IQ3_S, T_IQ3_S, T_IQ3_S, 500)):
+        assert not gpu.q4_hip_moe_exec(q4mi.ptr(ly.d_arena), ly.stride,
+                                       idh.ctypes.data_as(ctypes.c_void_p),
+                                       wh.ctypes.data_as(ctypes.c_void_p), 8, gt, ly.og, ut,
+                                       ly.ou, dt, ly.od, q4mi.ptr(dx), None, None, None,
+                                       q4mi.ptr(y), ff, ly.n_embd, ly.n_embd)
+    assert not gpu.q4_hip_moe_exec(q4mi.ptr(ly.d_arena), ly.stride,
+                                   idh.ctypes.data_as(ctypes.c_void_p),
+                                   wh.ctypes.data_as(ctypes.c_void_p), 65, T_IQ3_S, ly.og,
+                                   T_IQ3_S, ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx), None, None,
+                                   None, q4mi.ptr(y), ly.n_ff, ly.n_embd, ly.n_embd)
+    assert np.array_equal(host(y), before)
+
+
+@pytest.mark.parametrize("n_tok", [2, 4, 8])
+def test_moe_window_config3(gpu, oracle, n_tok):
+    """n_tok tokens (1 accepted + drafts), each with its
+    own top-10 + the shared expert; experts shared by tokens read once."""
+    ly = layer()
+    rng = np.random.default_rng(30 + n_tok)
+    x = rng.standard_normal((n_tok, ly.n_embd)).astype(np.float32)
+    es = np.full((n_tok, 64), -1, np.int32)
+    ew = np.zeros((n_tok, 64), np.float32)
+    nh = np.zeros(n_tok, np.int32)
+    all_ids, all_w = [], []
+    k = 10 if n_tok <= 4 else 6   # n_tok * (k + 1) <= 64 unique-entry bound
+    for t in range(n_tok):
+        ids, wts = routed_ids(oracle, rng, k=k)
+        ids = np.append(ids, 512)
+        wts = np.append(wts, 1.0)
+        es[t, :len(ids)], ew[t, :len(ids)], nh[t] = ids, wts, len(ids)
+        all_ids.append(ids)
+        all_w.append(wts)
+    assert gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, T_IQ3_S, ly.n_embd, ly.n_ff, n_tok)
+    d_es, d_ew, d_nh, dx = dev(es), dev(ew), dev(nh), dev(x)
+    y = dev(np.zeros((n_tok, ly.n_embd), np.float32))
+    ok = gpu.q4_hip_moe_exec_win(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es),
+                                 q4mi.ptr(d_ew), q4mi.ptr(d_nh), n_tok, T_IQ3_S, ly.og, T_IQ3_S,
+                                 ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx), None, q4mi.ptr(y),
+                                 ly.n_ff, ly.n_embd, ly.n_embd)
+    q4mi.check(ok, "q4_hip_moe_exec_win")
+    yo = oracle.moe_tokens(ly.n_embd, ly.n_ff, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x,
+                           np.array(all_ids, np.int32), np.array(all_w, np.float32))
+    assert rel_err(host(y), yo) <= TOL
