@@ -1,0 +1,267 @@
+"""Benchmark: IQ3_S routed-expert decode on one MI355X.
+
+A step is one decode token through a stack of L (default 48) MoE layers, each
+with its own 513 resident IQ3_S experts (512 routed + 1 shared; hidden 2048,
+expert intermediate 512), top-10 routing + the shared expert at weight 1.
+The stack holds L x 693 MB of distinct experts, far beyond the 256 MB
+Infinity Cache, so every layer streams its 11 experts from HBM.  The L layer
+calls (2 kernels each) are captured once in a HIP graph and replayed.
+
+value = sustained algorithmic GB/s per layer: (11 experts x 1,351,680 B +
+x 8 KB + y 8 KB) / layer time.  roofline = the gate/up kernel timed alone
+(its own graph of L launches), algorithmic bytes 11 x 901,120 + 8,192 per
+launch.  Also reported: single-layer latency, config 0 (IQ3_S 4096x4096
+GEMV) and config 4 (Q8_0 151936x2048 lm-head, n=1 and n=4).
+
+cpu_baseline: the reference's CPU expert job (q4_cpuex_dispatch2, compiled
+from its sources into oracle/_ref) on this host's cores, on the same layer
+shape; the repo's scalar C oracle when that build is absent.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "suzuku-engine-q4_amd"))
+
+METRIC = "IQ3_S MoE MMVQ GB/s (% of 8 TB/s) + prefill MMQ tok/s, 1 MI355X"
+HBM_PEAK = 8000.0  # GB/s
+N_EMBD, N_FF, N_EXP, TOPK = 2048, 512, 512, 10
+EXPERT_BYTES = 1351680
+LAYER_BYTES = 11 * EXPERT_BYTES + 2 * 4 * N_EMBD   # 14,884,864
+GU_BYTES = 11 * 901120 + 4 * N_EMBD
+
+
+def routes(rng, L):
+    import numpy as np
+    out = []
+    for _ in range(L):
+        lg = rng.standard_normal(N_EXP).astype(np.float32)
+        p = np.exp(lg - lg.max())
+        p /= p.sum()
+        ids = np.lexsort((np.arange(N_EXP), -lg))[:TOPK]
+        w = p[ids] / p[ids].sum()
+        out.append((np.append(ids, N_EXP).astype(np.int32),
+                    np.append(w, 1.0).astype(np.float32)))
+    return out
+
+
+def cpu_baseline(seconds=12.0):
+    """The reference CPU expert job on this host (bounded sample)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as om
+    from q4mi import synth
+    rng = np.random.default_rng(5)
+    arena = synth.expert_arena(rng, N_EXP + 1, N_EMBD, N_FF)
+    stride = synth.expert_stride(N_EMBD, N_FF)[0]
+    x = rng.standard_normal(N_EMBD).astype(np.float32)
+    rts = routes(rng, 64)
+    if om.have_ref():
+        R = om.Ref()
+        kind, cores = "reference", int(R.L.qref_threads())
+
+        def run(i):
+            ids, w = rts[i % len(rts)]
+            R.moe_decode(N_EMBD, N_FF, om.T_IQ3_S, om.T_IQ3_S, N_EXP + 1, arena, stride, x,
+                         ids, w)
+    else:
+        O = om.Oracle()
+        kind, cores = "port", 1
+
+        def run(i):
+            ids, w = rts[i % len(rts)]
+            O.moe_tokens(N_EMBD, N_FF, om.T_IQ3_S, om.T_IQ3_S, arena, stride, x, ids[None],
+                         w[None])
+    for i in range(3):
+        run(i)
+    times = []
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        run(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = float(np.median(times))
+    return {"value": round(LAYER_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": kind,
+            "sample": "%d config-2 decode layers (11 IQ3_S experts each, routes rotating over "
+                      "a 693 MB arena), median %.1f us/layer" % (len(times), med * 1e6)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the routed-expert path is a "
+              "single-GPU kernel set; multi-GPU sharding is a design note, not built).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import q4mi
+    from q4mi import synth
+
+    L = q4mi.lib()
+    torch.cuda.set_device(0)
+    q4mi.use_torch_stream()
+    L.q4_hip_moe_scratch_warm()
+    stride, og, ou, od = synth.expert_stride(N_EMBD, N_FF)
+    rng = np.random.default_rng(1234)
+    NL = args.layers
+    arenas = [synth.device_iq3s((N_EXP + 1) * stride, seed=1000 + l) for l in range(NL)]
+    xs = torch.randn(NL, N_EMBD, device="cuda", generator=torch.Generator("cuda").manual_seed(9))
+    ys = torch.zeros(NL, N_EMBD, device="cuda")
+    rts = routes(rng, NL)
+    T = q4mi.T_IQ3_S
+
+    def layer_call(l):
+        ids, w = rts[l]
+        ok = L.q4_hip_moe_exec(arenas[l].data_ptr(), stride, ids.ctypes.data_as(ctypes.c_void_p),
+                               w.ctypes.data_as(ctypes.c_void_p), len(ids), T, og, T, ou, T, od,
+                               xs[l].data_ptr(), None, None, None, ys[l].data_ptr(), N_FF,
+                               N_EMBD, N_EMBD)
+        q4mi.check(ok, "q4_hip_moe_exec")
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()   # eager warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            q4mi.use_torch_stream()
+            fn()
+        q4mi.use_torch_stream()
+        return g
+
+    def stack():
+        for l in range(NL):
+            layer_call(l)
+
+    def timed(g, steps, warmup):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    # replay vs eager: identical bits (no memset nodes; deterministic reduce)
+    g_full = capture(stack)
+    ys.zero_()
+    g_full.replay()
+    torch.cuda.synchronize()
+    y_graph = ys.clone()
+    ys.zero_()
+    stack()
+    torch.cuda.synchronize()
+    assert torch.equal(y_graph, ys), "graph replay differs from eager"
+
+    ms = timed(g_full, args.steps, args.warmup)
+    t_layer = ms * 1e-3 / (args.steps * NL)
+    value = LAYER_BYTES / t_layer / 1e9
+
+    # the gate/up kernel alone (dominant kernel: 2/3 of the bytes)
+    L.q4mi_moe_phases(1)
+    g_gu = capture(stack)
+    ms_gu = timed(g_gu, args.steps, args.warmup)
+    L.q4mi_moe_phases(2)
+    g_dn = capture(stack)
+    ms_dn = timed(g_dn, args.steps, args.warmup)
+    L.q4mi_moe_phases(3)
+    t_gu = ms_gu * 1e-3 / (args.steps * NL)
+    t_dn = ms_dn * 1e-3 / (args.steps * NL)
+    gu_gbs = GU_BYTES / t_gu / 1e9
+
+    # single-layer latency (eager, synchronised)
+    torch.cuda.synchronize()
+    lat = []
+    for i in range(50):
+        t0 = time.perf_counter()
+        layer_call(i % NL)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t0)
+    single_us = float(np.median(lat[5:])) * 1e6
+
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded IQ3_S experts generated in HBM; N(0,1) activations)",
+        "config": {"workload": "config 2: IQ3_S MoE decode layer, 1 token, hidden 2048, "
+                               "512 routed experts top-10 + 1 shared, expert intermediate 512; "
+                               "sustained over a %d-layer stack of distinct experts" % NL,
+                   "layers_per_step": NL, "bytes_per_layer": LAYER_BYTES},
+        "pct_of_hbm": round(100 * value / HBM_PEAK, 2),
+        "layer_us": round(t_layer * 1e6, 3),
+        "kernel_us": {"moe_gu_k": round(t_gu * 1e6, 3), "moe_dn_k": round(t_dn * 1e6, 3)},
+        "single_layer_latency_us": round(single_us, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 2), "peak": HBM_PEAK,
+                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "moe_gu_k", "bytes_per_launch": GU_BYTES},
+    }
+    del g_full, g_gu, g_dn, arenas
+    torch.cuda.empty_cache()
+
+    if not args.no_extra:
+        out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1)
+        out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
+                                              2048, 2, 1)
+        out["config4_lmhead_n4"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
+                                              2048, 2, 4)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):
+    """q4_mmvq_n over `copies` distinct weight copies (rotated to defeat the
+    Infinity Cache); GB/s = (weights + x + y) / kernel-pair time."""
+    rb = q4mi.row_bytes(ty, K)
+    gen = synth.device_iq3s if ty == q4mi.T_IQ3_S else synth.device_q80
+    ws = [gen(rows * rb, seed=77 + c) for c in range(copies)]
+    x = torch.randn(nt, K, device="cuda")
+    y = torch.empty(nt, rows, device="cuda")
+    L.q4_mmvq_warm()
+
+    def run():
+        for w in ws:
+            q4mi.check(L.q4_mmvq_n(ty, w.data_ptr(), rows, K, x.data_ptr(), y.data_ptr(), 1.0,
+                                   nt), "q4_mmvq_n")
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    nbytes = rows * rb + 4 * nt * K + 4 * nt * rows
+    del ws
+    return {"us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+            "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
+            "note": "includes the q8 quantize launch; eager launches"}
+
+
+if __name__ == "__main__":
+    main()

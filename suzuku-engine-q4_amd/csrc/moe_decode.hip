@@ -290,12 +290,19 @@ static bool dn_dispatch(MoeArgs a, const HostList &hl, uint32_t grid_u) {
     return false;
 }
 
+// Measurement hook: bit 0 runs the gate/up launch, bit 1 the down launch
+// (default both).  Lets a benchmark time each kernel of the pair alone.
+static int g_phases = 3;
+
 template <int NT>
 static bool run_nt(uint32_t ty_gu, uint32_t ty_dn, MoeArgs a, const HostList &hl,
                    uint32_t grid_u) {
-    bool ok = ty_gu == Q4MI_T_IQ3_S ? gu_dispatch<FmtIQ3S, NT>(a, hl, grid_u)
-                                    : gu_dispatch<FmtQ80, NT>(a, hl, grid_u);
-    if (!ok) return false;
+    if (g_phases & 1) {
+        const bool ok = ty_gu == Q4MI_T_IQ3_S ? gu_dispatch<FmtIQ3S, NT>(a, hl, grid_u)
+                                              : gu_dispatch<FmtQ80, NT>(a, hl, grid_u);
+        if (!ok) return false;
+    }
+    if (!(g_phases & 2)) return true;
     return ty_dn == Q4MI_T_IQ3_S ? dn_dispatch<FmtIQ3S, NT>(a, hl, grid_u)
                                  : dn_dispatch<FmtQ80, NT>(a, hl, grid_u);
 }
@@ -369,6 +376,9 @@ using namespace q4mi;
 extern "C" void q4_mmvq_warm(void);
 
 extern "C" {
+
+/* Benchmark hook: 1 = gate/up launch only, 2 = down only, 3 = both. */
+void q4mi_moe_phases(int mask) { g_phases = mask & 3; }
 
 /* Allocate the decode scratch (call before any stream capture). */
 void q4_hip_moe_scratch_warm(void) {
