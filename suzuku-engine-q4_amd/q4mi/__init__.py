@@ -51,6 +51,19 @@ _SIGS = {
     "q4_hip_moe_win_ok": (_b, [_u32, _u32, _u32, _u32, _u32, _u32]),
     "q4_hip_moe_exec_win": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
                                  _u64, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_route_pf": (_b, [_vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_softmax_topk_launch": (_b, [_vp, _u32, _u32, _vp, _vp]),
+    "q4_hip_softmax_topk": (_b, [_vp, _u32, _u32, _vp, _vp]),
+    "q4mi_assign": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "q4_hip_assign_pf": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "q4_hip_expert_reduce": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_mmq_on": (_c.c_int, []),
+    "q4_mmq_group": (_u32, []),
+    "q4_mmq_supported": (_b, [_u32, _u64]),
+    "q4_mmq_q8_bytes": (_u64, [_u64, _u64]),
+    "q4_mmq_quantize": (_b, [_vp, _vp, _vp, _u32, _u64, _u64]),
+    "q4_mmq_mul_id": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _vp, _u32, _u64, _vp, _u64]),
+    "q4_mmq_swiglu": (_b, [_vp, _vp, _u64, _u64]),
 }
 
 _lib = None

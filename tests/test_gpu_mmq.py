@@ -1,0 +1,156 @@
+"""GPU parity for the prefill MMQ path (q4_mmq_quantize / q4_mmq_mul_id /
+q4_mmq_swiglu / q4_hip_expert_reduce and the routing pack), against the C
+oracle.  fp32 outputs: max relative error <= 1e-3."""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+import oracle as om
+import q4mi
+from q4mi import synth
+
+pytestmark = pytest.mark.gpu
+T_IQ3_S, T_Q8_0 = q4mi.T_IQ3_S, q4mi.T_Q8_0
+TOL = 1e-3
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def zeros(shape, dtype=None):
+    import torch
+    return torch.zeros(shape, dtype=dtype or torch.float32, device="cuda")
+
+
+def mmq_quant(L, x, ids, cols, rows):
+    import torch
+    xq = zeros(int(L.q4_mmq_q8_bytes(rows, cols)), torch.uint8)
+    q4mi.check(L.q4_mmq_quantize(q4mi.ptr(x), q4mi.ptr(ids), q4mi.ptr(xq), T_IQ3_S, cols, rows),
+               "q4_mmq_quantize")
+    return xq
+
+
+def mul_id(L, w, ty, N, K, estride, n_exp, xq, bounds, total, ld):
+    dst = zeros((total, ld))
+    q4mi.check(L.q4_mmq_mul_id(q4mi.ptr(w), ty, N, K, estride, n_exp, q4mi.ptr(xq),
+                               q4mi.ptr(bounds), 0, total, q4mi.ptr(dst), ld), "q4_mmq_mul_id")
+    return dst
+
+
+@pytest.mark.parametrize("ty,N,K", [(T_IQ3_S, 1024, 2048), (T_IQ3_S, 2048, 512),
+                                    (T_Q8_0, 256, 2048), (T_Q8_0, 128, 512)])
+def test_mul_id_ragged(gpu, oracle, ty, N, K):
+    rng = np.random.default_rng(N + K + ty)
+    per = [100, 0, 1, 40, 64, 65, 3, 19]          # ragged, incl. empty and tile edges
+    E = len(per)
+    rb = om.row_bytes(ty, K)
+    W = synth.matrix(rng, ty, E * N, K)
+    estride = N * rb
+    T = 90
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    a_tok = np.concatenate([rng.integers(0, T, n) for n in per]).astype(np.int32)
+    bounds = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+    total = int(bounds[-1])
+    dx, dids = dev(x), dev(a_tok)
+    xq = mmq_quant(gpu, dx, dids, K, total)
+    dW, dbounds = dev(W), dev(bounds)
+    dst = host(mul_id(gpu, dW, ty, N, K, estride, E, xq, dbounds, total, N))
+    for e in range(E):
+        if per[e] == 0:
+            continue
+        rows = a_tok[bounds[e]:bounds[e + 1]]
+        ref = oracle.dot8_rows(ty, W[e * estride:(e + 1) * estride], N, K, x[rows])
+        assert rel_err(dst[bounds[e]:bounds[e + 1]], ref) <= TOL, e
+
+
+def test_mmq_group_sums_exact(gpu, oracle):
+    """With d_w = 1 and one activation group of d_x = 1/127 scale... the MMQ
+    output of a single 256-value row equals the oracle's exact integer sums."""
+    rng = np.random.default_rng(77)
+    N, K = 64, 256
+    W = synth.matrix(rng, T_IQ3_S, N, K)
+    Wb = W.reshape(-1, 110)
+    Wb[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    x = rng.integers(-127, 128, (3, K)).astype(np.float32)
+    x[:, ::32] = 127.0                               # amax 127 -> d = 1, q = x exactly
+    bounds = np.array([0, 3], np.int32)
+    dx, dW, dbounds = dev(x), dev(W), dev(bounds)
+    xq = mmq_quant(gpu, dx, None, K, 3)
+    dst = host(mul_id(gpu, dW, T_IQ3_S, N, K, N * 110, 1, xq, dbounds, 3, N))
+    for t in range(3):
+        q, d, _ = oracle.quant8(x[t])
+        assert np.all(d == 1.0) and np.array_equal(q.astype(np.float32), x[t])
+        for n in range(N):
+            s = oracle.group_sums(T_IQ3_S, W[n * 110:(n + 1) * 110], K, q)
+            assert dst[t, n] == float(s.sum())
+
+
+def test_prefill_layer_config3(gpu, oracle):
+    """BASELINE config 3-prefill: 2048 tokens, Zipf-skewed top-10 over 512
+    experts + the shared expert; route -> stable pack -> quantize ->
+    MMQ gate/up -> SwiGLU -> quantize -> MMQ down -> weighted reduce.
+    Checked on a sample of tokens against the oracle's composition."""
+    import torch
+    E, H, F, T, k = 512, 2048, 512, 2048, 10
+    rng = np.random.default_rng(3)
+    arena = synth.expert_arena(rng, E + 1, H, F)
+    stride, og, ou, od = synth.expert_stride(H, F)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    lg = synth.logits(rng, T, E, zipf=True)
+    d_arena, dx, dlg = dev(arena), dev(x), dev(lg)
+    L = gpu
+    ids, wts = zeros((T, k), torch.int32), zeros((T, k))
+    q4mi.check(L.q4_hip_route_pf(q4mi.ptr(dlg), q4mi.ptr(ids), q4mi.ptr(wts), T, E, k), "route")
+    a_tok, rsrc, rw = zeros(T * k, torch.int32), zeros(T * k, torch.int32), zeros(T * k)
+    stg, stgn, ek = zeros(512, torch.int32), zeros(1, torch.int32), zeros(512, torch.int32)
+    bounds = zeros(E + 1, torch.int32)
+    q4mi.check(L.q4mi_assign(q4mi.ptr(ids), q4mi.ptr(wts), q4mi.ptr(a_tok), q4mi.ptr(rsrc),
+                             q4mi.ptr(rw), q4mi.ptr(stg), q4mi.ptr(stgn), q4mi.ptr(ek),
+                             q4mi.ptr(bounds), T, k, E, T), "assign")
+    rows = T * k
+    # routed experts: gate|up are contiguous (gate rows then up rows) = one
+    # 2F x H matrix per expert at arena + e*stride
+    xq = mmq_quant(L, dx, a_tok, H, rows)
+    gu = mul_id(L, d_arena, T_IQ3_S, 2 * F, H, stride, E, xq, bounds, rows, 2 * F)
+    h = zeros((rows, F))
+    q4mi.check(L.q4_mmq_swiglu(q4mi.ptr(gu), q4mi.ptr(h), rows, F), "swiglu")
+    hq = mmq_quant(L, h, None, F, rows)
+    dn_w = d_arena[od:]
+    pd = mul_id(L, dn_w, T_IQ3_S, H, F, stride, E, hq, bounds, rows, H)
+    y = zeros((T, H))
+    q4mi.check(L.q4_hip_expert_reduce(q4mi.ptr(y), q4mi.ptr(pd), q4mi.ptr(rsrc), q4mi.ptr(rw),
+                                      T, k, H), "reduce")
+    # shared expert: one "expert" over all tokens, weight 1
+    sb = dev(np.array([0, T], np.int32))
+    sxq = mmq_quant(L, dx, None, H, T)
+    sgu = mul_id(L, d_arena[E * stride:], T_IQ3_S, 2 * F, H, stride, 1, sxq, sb, T, 2 * F)
+    sh = zeros((T, F))
+    q4mi.check(L.q4_mmq_swiglu(q4mi.ptr(sgu), q4mi.ptr(sh), T, F), "swiglu")
+    shq = mmq_quant(L, sh, None, F, T)
+    spd = mul_id(L, d_arena[E * stride + od:], T_IQ3_S, H, F, stride, 1, shq, sb, T, H)
+    ones = dev(np.ones(T, np.float32))
+    iden = dev(np.arange(T, dtype=np.int32))
+    q4mi.check(L.q4_hip_expert_reduce(q4mi.ptr(y), q4mi.ptr(spd), q4mi.ptr(iden), q4mi.ptr(ones),
+                                      T, 1, H), "reduce shared")
+    yg = host(y)
+    # routing and pack are bit-exact against the oracle
+    oid, ow = oracle.softmax_topk(lg, k)
+    assert np.array_equal(host(ids), oid)
+    pk = oracle.pack(oid, ow, E, T)
+    assert np.array_equal(host(a_tok), pk["a_tok"][:rows])
+    assert np.array_equal(host(bounds), pk["bounds"])
+    # sampled tokens through the oracle (routed picks + shared, weight 1)
+    samp = np.concatenate([[0, T - 1], rng.choice(np.arange(1, T - 1), 22, replace=False)])
+    sid = np.concatenate([oid[samp], np.full((len(samp), 1), E, np.int32)], 1)
+    sw = np.concatenate([ow[samp], np.ones((len(samp), 1), np.float32)], 1)
+    yo = oracle.moe_tokens(H, F, T_IQ3_S, T_IQ3_S, arena, stride, x[samp], sid, sw, mode=1)
+    assert rel_err(yg[samp], yo) <= TOL
