@@ -1,0 +1,165 @@
+/* q4mi.h -- C ABI of the MI355X (gfx950) routed-expert matmul library.
+ *
+ * Drop-in for the quantized routed-expert path of the reference engine's
+ * q4.h: the reference's C host (src/q4_moe.c) links these names unchanged in
+ * place of the dispatch in src/q4_rocm.cu / src/q4_mmq.cu / src/q4_mmvq.cu.
+ * Plain pointers and sizes only; every pointer named d_* is device memory.
+ * All launches are asynchronous on the stream returned by q4_hip_stream().
+ * A false return means "not covered / bad arguments": nothing was launched
+ * (the reference's reject-before-launch contract, src/q4_rocm.cu:5433-5438),
+ * and q4mi_last_error() says why.
+ *
+ * Weight formats: IQ3_S (ggml type 21, 110-byte superblocks of 256 values)
+ * and Q8_0 (type 8, 34-byte blocks of 32).  Experts are resident at
+ * base + slot*stride as gate[n_ff][in_dim] | up[n_ff][in_dim] |
+ * down[n_embd][n_ff] (reference src/q4_expert.c:962-982).
+ */
+#ifndef Q4MI_H
+#define Q4MI_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Stream of every launch.  Replaces q4_hip_stream (src/q4.h:1137,
+ * src/q4_rocm.cu:852). */
+void *q4_hip_stream(void);
+/* Select the launch stream (hipStream_t; NULL = the default stream).  No
+ * reference counterpart: the reference owned one global stream. */
+void q4mi_set_stream(void *stream);
+/* Text of the last rejection or launch failure. */
+const char *q4mi_last_error(void);
+/* 1 when a HIP device is visible. */
+int q4mi_device_ok(void);
+
+/* ------------------------------------------------------- q8 activations */
+
+/* Bit-exact CPU-expert quantizer (cpx_quant8, src/q4_cpuexp.c:605-637) on
+ * the GPU: rows of `cols` fp32 (row r = x[ids ? ids[r] : r]) -> int8 codes
+ * q[rows][cols], fp32 scales d[rows][cols/32], int32 code sums
+ * bs[rows][cols/32] (bs may be NULL).  cols % 32 == 0. */
+bool q4mi_quant8(const float *d_x, const int32_t *d_ids, uint64_t rows, uint64_t cols,
+                 int8_t *d_q, float *d_d, int32_t *d_bs);
+
+/* ---------------------------------------------------------- dense MMVQ */
+
+/* Replaces q4_mmvq_on/_set/_verify/_warm/_hold/_release/q4_mmvq_n
+ * (src/q4.h:914-927, src/q4_mmvq.cu:266-349), extended to IQ3_S and Q8_0:
+ * y[t*nrows + r] = scale * (W_r . q8(x_t)), t < n (1..8).  A row's result
+ * does not depend on n.  ncols/32 in {8,16,32,64,128,256}. */
+int q4_mmvq_on(void);
+void q4_mmvq_set(int v);
+void q4_mmvq_verify(int on);
+void q4_mmvq_warm(void);
+void q4_mmvq_hold(const float *d_x);
+void q4_mmvq_release(void);
+bool q4_mmvq_n(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
+               const float *d_x, float *d_y, float scale, uint32_t n);
+/* Pre-quantized activations (the q4mi_quant8 layout); d_sums (optional)
+ * receives the exact int32 group sums (2s+1)*sum(w*q) at
+ * [(t*nrows + r)*(ncols/32) + g].  No reference counterpart (debug export of
+ * the per-block accumulators the CPU path keeps in registers,
+ * src/q4_cpuexp.c:855-892). */
+bool q4mi_mmvq(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
+               const int8_t *d_xq, const float *d_xd, uint32_t n, float *d_y, float scale,
+               int32_t *d_sums);
+
+/* ------------------------------------------------- routed-expert decode */
+
+/* Size library scratch before any graph capture (src/q4.h:958). */
+void q4_hip_moe_scratch_warm(void);
+/* Measurement hook: 1 = gate/up launch only, 2 = down only, 3 = both
+ * (default).  No reference counterpart. */
+void q4mi_moe_phases(int mask);
+/* One token; slots/wts are HOST arrays of n <= 64 experts.
+ * d_y[r] += sum_e wts[e] * down_e(q8(silu(gate_e.q8(x)) * up_e.q8(x))).
+ * gt == ut; IQ3_S or Q8_0; in_dim == n_embd.  d_h, d_h2, d_down are
+ * accepted for ABI compatibility and unused.  Replaces q4_hip_moe_exec
+ * (src/q4.h:951-956, src/q4_rocm.cu:5425-5470). */
+bool q4_hip_moe_exec(const uint8_t *base, uint64_t stride, const int32_t *slots,
+                     const float *wts, uint32_t n, uint32_t gt, uint64_t og, uint32_t ut,
+                     uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_h,
+                     float *d_h2, float *d_down, float *d_y, uint32_t n_ff, uint32_t in_dim,
+                     uint32_t n_embd);
+/* Same with device lists (count d_nhit[0]); graph-capturable.  Replaces
+ * q4_hip_moe_exec_dev (src/q4.h:1295-1301, src/q4_rocm.cu:6570-6608). */
+bool q4_hip_moe_exec_dev(const uint8_t *base, uint64_t stride, const int32_t *d_es,
+                         const float *d_ew, const int32_t *d_nhit, uint32_t gt, uint64_t og,
+                         uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od, const float *d_x,
+                         float *d_h, float *d_h2, float *d_down, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd);
+/* Verify window, 2..8 tokens; token t's picks at d_es/d_ew[t*64 ..
+ * t*64 + d_nh[t]); experts picked by several tokens are read once.  x, y
+ * token-major.  Replaces q4_hip_moe_win_ok / q4_hip_moe_exec_win
+ * (src/q4.h:906-913, src/q4_rocm.cu:7369-7531); covers every IQ3_S/Q8_0
+ * layer (the reference required an IQ4_NL/Q2_0 down). */
+bool q4_hip_moe_win_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uint32_t n_ff,
+                       uint32_t n_tok);
+bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_es,
+                         const float *d_ew, const int32_t *d_nh, uint32_t n_tok, uint32_t gt,
+                         uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
+                         const float *d_x, float *d_h, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd);
+
+/* ------------------------------------------------------ routing and pack */
+
+/* Per-token softmax + top-k + renormalisation (q4_softmax + q4_topk,
+ * src/q4_quant.c:715-755); n_exp <= 512, topk 1..64.  Replaces
+ * q4_hip_route_pf (src/q4.h:1278-1280, src/q4_rocm.cu:6383-6549). */
+bool q4_hip_route_pf(const float *d_rlog, int32_t *d_ids, float *d_wts, uint32_t n_tok,
+                     uint32_t n_exp, uint32_t topk);
+/* Single token variants (src/q4.h:1414-1418, src/q4_rocm.cu:12703-12789). */
+bool q4_hip_softmax_topk_launch(const float *d_logits, uint32_t n, uint32_t k, int32_t *d_ids,
+                                float *d_wts);
+bool q4_hip_softmax_topk(const float *d_logits, uint32_t n, uint32_t k, int32_t *h_ids,
+                         float *h_wts);
+/* Stable expert pack per token group: the host order of src/q4_moe.c:
+ * 3404-3451 (the reference's GPU assign_pf_k orders by atomic arrival).
+ * Replaces q4_hip_assign_pf (src/q4.h:1281-1285, src/q4_rocm.cu:6483-6563). */
+bool q4_hip_assign_pf(const int32_t *d_ids, const float *d_wts, int32_t *d_atok,
+                      int32_t *d_rsrc, float *d_rw, int32_t *d_stg, uint32_t *d_stgn,
+                      uint32_t *d_ek, uint32_t gsz, uint32_t topk, uint32_t n_exp,
+                      uint32_t n_tok);
+/* Same plus the MMQ expert bounds [n_g][n_exp+1] the reference built on the
+ * host (src/q4_moe.c:3558-3571); d_bounds may be NULL. */
+bool q4mi_assign(const int32_t *d_ids, const float *d_wts, int32_t *d_atok, int32_t *d_rsrc,
+                 float *d_rw, int32_t *d_stg, uint32_t *d_stgn, uint32_t *d_ek,
+                 int32_t *d_bounds, uint32_t gsz, uint32_t topk, uint32_t n_exp,
+                 uint32_t n_tok);
+/* dy[t] += sum_k rw[t,k] * pd[rsrc[t,k]] in k order (deterministic).
+ * Replaces q4_hip_expert_reduce (src/q4.h:1087-1089,
+ * src/q4_rocm.cu:15739-15761). */
+bool q4_hip_expert_reduce(float *d_y, const float *d_pd, const int32_t *d_rsrc,
+                          const float *d_rw, uint32_t n_tok, uint32_t topk, uint32_t n_embd);
+
+/* ------------------------------------------------------------ prefill MMQ */
+
+/* Replaces the q4_mmq_* wrapper around vendored ggml MMQ
+ * (src/q4.h:1150-1175, src/q4_mmq.cu:250-610).  Types IQ3_S, Q8_0;
+ * w_rows % 64 == 0, w_cols % 256 == 0.  The activation buffer layout is this
+ * library's (q4_mmq_q8_bytes gives its size); its codes are the bit-exact
+ * CPU-expert q8 codes.  The slot-gather helpers (q4_mmq_wbuf*, q4_mmq_gather,
+ * q4_mmq_pad) have no counterpart: every expert is resident and MMQ reads it
+ * in place at w + e*expert_stride_bytes. */
+int q4_mmq_on(void);
+uint32_t q4_mmq_group(void);
+bool q4_mmq_supported(uint32_t type, uint64_t w_rows);
+uint64_t q4_mmq_q8_bytes(uint64_t rows, uint64_t cols);
+bool q4_mmq_quantize(const float *x, const int32_t *ids, void *xq, uint32_t w_type,
+                     uint64_t cols, uint64_t rows);
+bool q4_mmq_mul_id(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_cols,
+                   uint64_t expert_stride_bytes, uint32_t n_expert, const void *xq,
+                   const int32_t *bounds, uint32_t max_rows, uint64_t total_rows, float *dst,
+                   uint64_t ld_dst);
+bool q4_mmq_swiglu(const float *gu, float *h, uint64_t rows, uint64_t n_ff);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4MI_H */

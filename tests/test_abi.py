@@ -1,0 +1,69 @@
+"""The C-ABI library: it loads without a GPU, exports every entry point the
+public header declares, the Python mirror binds the same set, and host-side
+argument checks reject bad calls before any device work (no GPU needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+import q4mi
+
+HEADER = os.path.join(ROOT, "include", "q4mi.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(q4(?:mi)?_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for must in ("q4_hip_moe_exec", "q4_hip_moe_exec_win", "q4_mmvq_n", "q4_mmq_mul_id",
+                 "q4_hip_route_pf", "q4_hip_assign_pf", "q4_hip_expert_reduce", "q4mi_quant8"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(q4mi.LIB_PATH), "build the library first"
+    out = subprocess.run(["nm", "-D", "--defined-only", q4mi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(l.split()[-1] for l in out.splitlines() if " T " in l)
+    missing = [n for n in declared() if n not in exported]
+    assert not missing, missing
+
+
+def test_python_mirror_binds_header():
+    assert set(q4mi.exported_symbols()) == set(declared())
+
+
+def test_loads_and_rejects_without_gpu():
+    L = q4mi.lib()
+    # host-side shape/type checks run before any HIP call
+    assert not L.q4_mmvq_n(99, 1, 16, 2048, 1, 1, 1.0, 1)
+    assert not L.q4_mmvq_n(q4mi.T_IQ3_S, 1, 16, 2000, 1, 1, 1.0, 1)
+    assert not L.q4_mmvq_n(q4mi.T_IQ3_S, 1, 16, 2048, 1, 1, 1.0, 9)
+    assert "not covered" in q4mi.last_error()
+    assert not L.q4_hip_moe_win_ok(q4mi.T_IQ3_S, q4mi.T_IQ3_S, q4mi.T_IQ3_S, 2048, 512, 1)
+    assert not L.q4_hip_moe_win_ok(q4mi.T_IQ3_S, q4mi.T_IQ3_S, q4mi.T_IQ3_S, 2048, 512, 9)
+    assert L.q4_hip_moe_win_ok(q4mi.T_IQ3_S, q4mi.T_IQ3_S, q4mi.T_IQ3_S, 2048, 512, 4)
+    assert not L.q4_hip_route_pf(1, 1, 1, 4, 513, 10)
+    assert not L.q4_hip_route_pf(1, 1, 1, 4, 512, 65)
+    assert not L.q4mi_assign(1, 1, 1, 1, 1, 1, 1, 1, None, 8, 0, 512, 4)
+    assert L.q4_mmq_supported(q4mi.T_IQ3_S, 1024)
+    assert not L.q4_mmq_supported(q4mi.T_IQ3_S, 1000)
+    assert not L.q4_mmq_supported(12, 1024)
+    assert L.q4_mmq_q8_bytes(10, 2048) == 10 * 2048 * 2 + 10 * 64 * 4 + 256
+    assert not L.q4_mmq_mul_id(1, q4mi.T_IQ3_S, 1000, 2048, 0, 8, 16, 1, 0, 10, 16, 1000)
+    ids = (ctypes.c_int32 * 65)()
+    w = (ctypes.c_float * 65)()
+    # 65 experts exceeds the per-call bound (src/q4_test.c:1652-1663)
+    assert not L.q4_hip_moe_exec(1, 0, ids, w, 65, 21, 0, 21, 0, 21, 0, 16, None, None, None,
+                                 16, 512, 2048, 2048)
+    assert not L.q4_hip_moe_exec(1, 0, ids, w, 0, 21, 0, 21, 0, 21, 0, 16, None, None, None,
+                                 16, 512, 2048, 2048)
