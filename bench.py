@@ -101,6 +101,7 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the routed-expert path is a "
@@ -222,6 +223,8 @@ def main():
     del g_full, g_gu, g_dn, arenas
     torch.cuda.empty_cache()
 
+    if not args.no_prefill:
+        out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
     if not args.no_extra:
         out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1)
         out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
@@ -231,6 +234,95 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
+
+
+PF_T, PF_K = 2048, 10
+PF_OPS = (PF_T * PF_K + PF_T) * 2 * 3 * N_EMBD * N_FF   # 141.7 G (routed + shared)
+
+
+def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
+    """Config 3-prefill: 2048 tokens, Zipf-skewed top-10 over 512 experts +
+    the shared expert, one MoE layer: route -> stable pack -> q8(x) ->
+    MMQ gate/up -> SwiGLU -> q8(h) -> MMQ down -> weighted reduce.  `copies`
+    distinct 693 MB layers rotate so weights stream from HBM."""
+    T, k, E, H, F = PF_T, PF_K, N_EXP, N_EMBD, N_FF
+    stride, og, ou, od = synth.expert_stride(H, F)
+    rows = T * k
+    rng = np.random.default_rng(99)
+    arenas = [synth.device_iq3s((E + 1) * stride, seed=500 + c) for c in range(copies)]
+    x = torch.randn(T, H, device="cuda")
+    lg = torch.from_numpy(synth.logits(rng, T, E, zipf=True)).cuda()
+    i32 = torch.int32
+    ids, wts = torch.empty(T, k, dtype=i32, device="cuda"), torch.empty(T, k, device="cuda")
+    a_tok, rsrc = torch.empty(rows, dtype=i32, device="cuda"), torch.empty(rows, dtype=i32,
+                                                                            device="cuda")
+    rw = torch.empty(rows, device="cuda")
+    stg, stgn = torch.empty(512, dtype=i32, device="cuda"), torch.empty(1, dtype=i32, device="cuda")
+    ek, bounds = torch.empty(512, dtype=i32, device="cuda"), torch.empty(E + 1, dtype=i32,
+                                                                         device="cuda")
+    xq = torch.empty(int(L.q4_mmq_q8_bytes(rows, H)), dtype=torch.uint8, device="cuda")
+    hq = torch.empty(int(L.q4_mmq_q8_bytes(rows, F)), dtype=torch.uint8, device="cuda")
+    pd = torch.empty(rows, H, device="cuda")
+    sb = torch.tensor([0, T], dtype=i32, device="cuda")
+    iden = torch.arange(T, dtype=i32, device="cuda")
+    ones = torch.ones(T, device="cuda")
+    y = torch.zeros(T, H, device="cuda")
+    P = q4mi.ptr
+    TY = q4mi.T_IQ3_S
+    chk = q4mi.check
+
+    hq_s = torch.empty(int(L.q4_mmq_q8_bytes(T, F)), dtype=torch.uint8, device="cuda")
+
+    def layer(c):
+        A = arenas[c].data_ptr()
+        chk(L.q4_hip_route_pf(P(lg), P(ids), P(wts), T, E, k), "route")
+        chk(L.q4mi_assign(P(ids), P(wts), P(a_tok), P(rsrc), P(rw), P(stg), P(stgn), P(ek),
+                          P(bounds), T, k, E, T), "assign")
+        # q8(x) once per token; routed rows gather it through a_tok
+        chk(L.q4_mmq_quantize(P(x), None, P(xq), TY, H, T), "q8 x")
+        chk(L.q4mi_mmq_gate_up(A, TY, F, H, stride, E, P(xq), T, P(a_tok), P(bounds), rows,
+                               P(hq)), "mmq gate/up")
+        chk(L.q4_mmq_mul_id(A + od, TY, H, F, stride, E, P(hq), P(bounds), 0, rows, P(pd), H),
+            "mmq down")
+        chk(L.q4_hip_expert_reduce(P(y), P(pd), P(rsrc), P(rw), T, k, H), "reduce")
+        # shared expert: every token, weight 1
+        S = A + E * stride
+        chk(L.q4mi_mmq_gate_up(S, TY, F, H, stride, 1, P(xq), T, None, P(sb), T, P(hq_s)),
+            "mmq gate/up shared")
+        chk(L.q4_mmq_mul_id(S + od, TY, H, F, stride, 1, P(hq_s), P(sb), 0, T, P(pd), H),
+            "mmq down shared")
+        chk(L.q4_hip_expert_reduce(P(y), P(pd), P(iden), P(ones), T, 1, H), "reduce shared")
+
+    def run_all():
+        for c in range(copies):
+            layer(c)
+
+    run_all()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q4mi.use_torch_stream()
+        run_all()
+    q4mi.use_torch_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    used = int((ek > 0).sum().item())
+    wbytes = (used + 1) * EXPERT_BYTES
+    del arenas
+    return {"layer_us": round(t * 1e6, 1), "tok_per_s": round(T / t, 1),
+            "mmq_TOPS": round(PF_OPS / t / 1e12, 2),
+            "pct_of_int8_peak": round(100 * PF_OPS / t / 5.0e15, 2),
+            "experts_touched": used, "weight_bytes": wbytes,
+            "weight_GB_per_s": round(wbytes / t / 1e9, 1),
+            "note": "whole routed layer incl. route, pack, quantize, SwiGLU, reduce and the "
+                    "shared expert; ops = (20480 + 2048) rows x 3 x 2048 x 512 x 2"}
 
 
 def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):

@@ -141,7 +141,9 @@ bool q4_hip_expert_reduce(float *d_y, const float *d_pd, const int32_t *d_rsrc,
 
 /* Replaces the q4_mmq_* wrapper around vendored ggml MMQ
  * (src/q4.h:1150-1175, src/q4_mmq.cu:250-610).  Types IQ3_S, Q8_0;
- * w_rows % 64 == 0, w_cols % 256 == 0.  The activation buffer layout is this
+ * w_rows % 128 == 0, w_cols % 256 == 0.  Weight buffers must be readable up
+ * to the next 4-byte boundary after their last byte (any hipMalloc'd
+ * buffer is).  The activation buffer layout is this
  * library's (q4_mmq_q8_bytes gives its size); its codes are the bit-exact
  * CPU-expert q8 codes.  The slot-gather helpers (q4_mmq_wbuf*, q4_mmq_gather,
  * q4_mmq_pad) have no counterpart: every expert is resident and MMQ reads it
@@ -157,6 +159,23 @@ bool q4_mmq_mul_id(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_col
                    const int32_t *bounds, uint32_t max_rows, uint64_t total_rows, float *dst,
                    uint64_t ld_dst);
 bool q4_mmq_swiglu(const float *gu, float *h, uint64_t rows, uint64_t n_ff);
+/* q4_mmq_mul_id with activation rows gathered through act_row: xq holds
+ * xrows rows (one per token, quantized once) and packed row p reads row
+ * act_row[p] (the pack's a_tok).  No reference counterpart: it removes the
+ * per-routed-row q8 copy the reference's quantize(x, ids) makes. */
+bool q4mi_mmq_mul_id_rows(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_cols,
+                          uint64_t expert_stride_bytes, uint32_t n_expert, const void *xq,
+                          uint64_t xrows, const int32_t *act_row, const int32_t *bounds,
+                          uint64_t total_rows, float *dst, uint64_t ld_dst);
+/* Fused gate/up: each expert's [gate; up] (2*n_ff x w_cols) against xq rows
+ * (through act_row when given); writes q8(silu(gate)*up) straight into hq
+ * (a q4_mmq_q8_bytes(total_rows, n_ff) buffer for the down mul_id).
+ * Replaces mul_id(gate|up) + q4_mmq_swiglu + q4_mmq_quantize(h)
+ * (src/q4_moe.c:3718-3730).  n_ff % 64 == 0. */
+bool q4mi_mmq_gate_up(const void *w, uint32_t type, uint64_t n_ff, uint64_t w_cols,
+                      uint64_t expert_stride_bytes, uint32_t n_expert, const void *xq,
+                      uint64_t xrows, const int32_t *act_row, const int32_t *bounds,
+                      uint64_t total_rows, void *hq);
 
 #ifdef __cplusplus
 }

@@ -1,7 +1,7 @@
 // Expert-sorted prefill MMQ on MFMA (gfx950).
 //
 // Routed rows are packed per expert (ragged bounds[e]..bounds[e+1]).  For
-// each (expert, 64-row token tile, 64-row weight tile) a 256-thread block
+// each (expert, 128-row token tile, 128-row weight tile) a 256-thread block
 // walks K one IQ3_S superblock (256 values) at a time:
 //   * weights: IQ3_S -> exact integers w*(2s+1) (|v| <= 465), written to LDS
 //     as fp16 (exact); Q8_0 -> its int8 values as fp16 (exact);
@@ -32,10 +32,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace q4mi {
 
-constexpr int MT = 64;          // token rows per block tile
-constexpr int NTW = 64;         // weight rows per block tile
-constexpr int KS = 256;         // K values per step (one IQ3_S superblock)
-constexpr int LDH = KS + 8;     // fp16 row stride in LDS (16-byte skew)
+constexpr int MT = 128;         // token rows per tile (the tile list's granularity)
 
 // ------------------------------------------------------------ quantizer
 // MMQ activation buffer layout: codes as fp16 [rows][cols], then fp32 group
@@ -65,7 +62,7 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 }
 
 // --------------------------------------------------------------- tiles
-// tiles[i] = (expert, first row of the 64-row tile); tiles[-1 slot] count.
+// tiles[i] = (expert, first row of its MT-row tile); *count = number of tiles.
 __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ bounds,
                                                    uint32_t n_exp, int2 *__restrict__ tiles,
                                                    uint32_t *__restrict__ count,
@@ -92,78 +89,136 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
 }
 
 // --------------------------------------------------------------- kernel
-struct Fp16Lds {
-    _Float16 w[NTW][LDH];    // weights of this K step (fp16 exact integers)
-    _Float16 x[MT][LDH];     // activation codes
-    float dx[8][MT];         // activation group scales
-    float dwg[8][NTW];       // Q8_0: per-group weight scales
-    float dwb[NTW];          // IQ3_S: superblock scale per weight row
-    uint2 g16[512];          // IQ3_S grid as fp16 magnitudes (4 halves)
-    uint2 sm16[16];          // sign nibble -> fp16 sign-bit masks
+// Block = 256 threads (4 waves), tile = 128 weight rows x 128 token rows.
+// Wave w owns weight rows [32w, 32w+32) of the tile and every token of it
+// (four 32-token sub-tiles, skipped when empty).  Each K superblock:
+//   1. the 128 rows' raw block bytes are copied to LDS with dword loads;
+//   2. per half superblock the 128 token rows' fp16 codes are copied to LDS;
+//   3. per 32-value group each lane decodes the 16 weight values its MFMA A
+//      operand needs straight from the raw bytes (lane half kh takes values
+//      8kh..8kh+7 and 16+8kh..+7), then two 32x32x16 MFMAs per token sub-tile.
+// Fused gate/up mode: tile rows 0..63 are gate rows n0..n0+63 and 64..127
+// the matching up rows F+n0..; waves 2,3 hand their accumulators to waves
+// 0,1 through LDS, which form h = silu(g)*u and write its q8 codes (the
+// 32 h columns of a q8 group are in the lane and its partner lane l^32).
+constexpr int MMQ_NB = 128;      // weight rows per block
+constexpr int MMQ_MB = 128;      // token rows per block
+constexpr int MMQ_KH = 128;      // K values per activation stage
+constexpr int MMQ_ALD = MMQ_KH + 8;  // fp16 row stride of the activation tile
+
+template <uint32_t TY>
+struct RawSpec {
+    static constexpr uint32_t SB = TY == Q4MI_T_IQ3_S ? 110u : 8u * 34u;  // bytes / 256 values
+    static constexpr uint32_t SS = (SB + 2u + 3u) / 4u * 4u;            // LDS slot bytes
 };
 
-__device__ inline uint32_t ld_u16(const uint8_t *p) { return *(const uint16_t *)p; }
-
-// Decode one IQ3_S 32-group of a weight row (global bytes, 2-aligned) into
-// 32 fp16 values w*(2s+1) at dst.
-__device__ inline void iq3s_group_f16(const Fp16Lds &L, const uint8_t *blk, uint32_t j,
-                                      _Float16 *dst) {
-    const uint8_t *qs = blk + 2 + 8 * j;
-    const uint32_t q0 = ld_u16(qs) | (ld_u16(qs + 2) << 16);
-    const uint32_t q1 = ld_u16(qs + 4) | (ld_u16(qs + 6) << 16);
-    const uint32_t qh = blk[66 + j];
-    const uint32_t sg = ld_u16(blk + 74 + 4 * j) | (ld_u16(blk + 76 + 4 * j) << 16);
-    const uint32_t sc = blk[106 + (j >> 1)];
-    const float m = (float)(2u * ((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1u);
-    const half2_t mm = {(_Float16)m, (_Float16)m};
-    uint4 out[4];
-    uint32_t *o = (uint32_t *)out;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t qb = ((k < 4 ? q0 : q1) >> (8 * (k & 3))) & 0xffu;
-        const uint32_t idx = qb | (((qh >> k) & 1u) << 8);
-        const uint2 g = L.g16[idx];
-        const uint2 s = L.sm16[(sg >> (4 * k)) & 15u];
-        half2_t a = __builtin_bit_cast(half2_t, g.x ^ s.x);
-        half2_t b = __builtin_bit_cast(half2_t, g.y ^ s.y);
-        a = a * mm;
-        b = b * mm;
-        o[2 * k] = __builtin_bit_cast(uint32_t, a);
-        o[2 * k + 1] = __builtin_bit_cast(uint32_t, b);
-    }
-    uint4 *d4 = (uint4 *)dst;
-#pragma unroll
-    for (int i = 0; i < 4; i++) d4[i] = out[i];
-}
+template <uint32_t TY>
+struct MmqLds {
+    _Float16 act[MMQ_MB][MMQ_ALD];          // 34.8 KB; reused for the fused hand-off
+    float dx[4][MMQ_MB];                    // group scales of the staged half
+    uint8_t raw[MMQ_NB][RawSpec<TY>::SS];   // raw weight bytes of this superblock
+    float dwb[MMQ_NB];                      // IQ3_S superblock scale per row
+    float dwg[8][MMQ_NB];                   // Q8_0 block scales per row
+    uint2 g16[512];                         // IQ3_S grid as fp16 magnitudes
+    uint2 sm16[16];                         // sign nibble -> fp16 sign masks
+};
 
 struct MmqArgs {
     const uint8_t *w;
     uint64_t estride;       // bytes between experts
     uint32_t rb;            // bytes per weight row
-    uint32_t K, N;          // w_cols, w_rows
-    const _Float16 *xq;     // [xrows][K]
+    uint32_t K;             // w_cols
+    uint32_t n_ff;          // fused mode: gate rows = up rows = n_ff
+    const _Float16 *xq;     // [xrows][K] fp16 codes
     const float *xd;        // [xrows][K/32]
     const int32_t *act_row; // optional: activation row of packed row p
     const int32_t *bounds;  // [n_exp+1]
     const int2 *tiles;
     const uint32_t *ntiles;
-    float *dst;
+    float *dst;             // plain mode: [rows][ld]
     uint64_t ld;
+    _Float16 *hq;           // fused mode: [rows][n_ff] fp16 codes of h
+    float *hd;              // fused mode: [rows][n_ff/32]
 };
 
+__device__ inline uint32_t lds_u16(const uint8_t *p) { return *(const uint16_t *)p; }
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+// Lane's A operands of group j for one weight row: A0 = values 8kh..8kh+7,
+// A1 = values 16+8kh..16+8kh+7 (IQ3_S entries 2kh, 2kh+1 / 4+2kh, 5+2kh).
 template <uint32_t TY>
+__device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t j,
+                                uint32_t kh, half8_t &A0, half8_t &A1) {
+    if (TY == Q4MI_T_IQ3_S) {
+        const uint32_t qa = lds_u16(R + 2 + 8 * j + 2 * kh);       // qs entries 2kh, 2kh+1
+        const uint32_t qb = lds_u16(R + 2 + 8 * j + 4 + 2 * kh);   // 4+2kh, 5+2kh
+        const uint32_t qh = R[66 + j];
+        const uint32_t sa = R[74 + 4 * j + kh];                    // sign nibbles 2kh, 2kh+1
+        const uint32_t sb = R[74 + 4 * j + 2 + kh];                // 4+2kh, 5+2kh
+        const uint32_t sc = R[106 + (j >> 1)];
+        const float m = (float)(2u * ((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1u);
+        const half2_t mm = {(_Float16)m, (_Float16)m};
+        uint32_t o[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t e = (q < 2 ? 2 * kh : 4 + 2 * kh) + (q & 1);  // entry index
+            const uint32_t qs8 = ((q < 2 ? qa : qb) >> (8 * (q & 1))) & 0xffu;
+            const uint32_t idx = qs8 | (((qh >> e) & 1u) << 8);
+            const uint32_t nib = ((q < 2 ? sa : sb) >> (4 * (q & 1))) & 15u;
+            const uint2 g = L.g16[idx];
+            const uint2 s = L.sm16[nib];
+            half2_t a = __builtin_bit_cast(half2_t, g.x ^ s.x) * mm;
+            half2_t b = __builtin_bit_cast(half2_t, g.y ^ s.y) * mm;
+            o[2 * q] = __builtin_bit_cast(uint32_t, a);
+            o[2 * q + 1] = __builtin_bit_cast(uint32_t, b);
+        }
+        A0 = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+        A1 = __builtin_bit_cast(half8_t, make_uint4(o[4], o[5], o[6], o[7]));
+    } else {
+        // Q8_0 block j of the superblock: qs at 34j+2; values 8kh.. and 16+8kh..
+        const uint8_t *qs = R + 34 * j + 2;
+        uint32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t off = (q < 2 ? 8 * kh : 16 + 8 * kh) + 4 * (q & 1);
+            v[q] = lds_u16(qs + off) | (lds_u16(qs + off + 2) << 16);
+        }
+        uint32_t o[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const _Float16 lo = (_Float16)(float)(int8_t)(v[q] >> (16 * b));
+                const _Float16 hi = (_Float16)(float)(int8_t)(v[q] >> (16 * b + 8));
+                o[2 * q + b] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+            }
+        }
+        A0 = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+        A1 = __builtin_bit_cast(half8_t, make_uint4(o[4], o[5], o[6], o[7]));
+    }
+}
+
+template <uint32_t TY, bool FUSED>
 __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    Fp16Lds &L = *(Fp16Lds *)smem;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    MmqLds<TY> &L = *(MmqLds<TY> *)smem;
+    constexpr uint32_t SB = RawSpec<TY>::SB;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6, kh = lane >> 5;
     const uint32_t ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int2 tinfo = a.tiles[ti];
     const uint32_t e = (uint32_t)tinfo.x;
     const int32_t rbase = a.bounds[e] + tinfo.y;
-    const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), (uint32_t)MT);
-    const uint32_t n0 = blockIdx.x * NTW;
-    const uint8_t *W = a.w + (uint64_t)e * a.estride + (uint64_t)n0 * a.rb;
+    const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), (uint32_t)MMQ_MB);
+    const uint32_t nts = (mrows + 31) / 32;    // token sub-tiles with rows
+    const uint8_t *We = a.w + (uint64_t)e * a.estride;
+    // weight row (within the expert) of tile row r
+    const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
+    auto wrow = [&](uint32_t r) -> uint32_t {
+        return FUSED ? (r < 64 ? nblk + r : a.n_ff + nblk + (r - 64)) : nblk + r;
+    };
 
     if (TY == Q4MI_T_IQ3_S) {
         for (uint32_t i = tid; i < 512; i += 256) {
@@ -177,112 +232,176 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
             L.g16[i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }
         if (tid < 16) {
-            uint32_t s[4];
+            uint32_t sgn[4];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) s[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
-            L.sm16[tid] = make_uint2(s[0] | (s[1] << 16), s[2] | (s[3] << 16));
+            for (int jj = 0; jj < 4; jj++) sgn[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
+            L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
         }
     }
-    // activation rows of this tile (packed row -> source row)
-    const uint32_t xr_lane = tid >> 2;      // 64 rows, 4 threads per row
+    // activation source row of this thread's staging slot (2 threads per row)
+    const uint32_t st_row = tid >> 1, st_half = tid & 1u;
     int64_t xrow = -1;
-    if (xr_lane < mrows) {
-        const int32_t p = rbase + (int32_t)xr_lane;
+    if (st_row < mrows) {
+        const int32_t p = rbase + (int32_t)st_row;
         xrow = a.act_row ? a.act_row[p] : p;
     }
-    const uint32_t wn = wv & 1u, wm = wv >> 1;   // wave's 32x32 output sub-tile
-    f32x16_t acc = {};
-    f32x16_t inner = {};
-    const uint32_t nsteps = a.K / KS;
-    for (uint32_t st = 0; st < nsteps; st++) {
-        __syncthreads();   // previous step's LDS reads are done
-        // activations: 64 rows x 256 fp16 (512 B per row), 4 threads per row
-        {
-            const uint32_t part = tid & 3u;
-            uint4 *dst = (uint4 *)&L.x[xr_lane][part * 64];
-            if (xrow >= 0) {
-                const uint4 *src = (const uint4 *)(a.xq + (uint64_t)xrow * a.K + st * KS + part * 64);
+    // raw staging: 2 threads per weight row
+    const uint32_t rw_row = tid >> 1, rw_part = tid & 1u;
+    const uint8_t *wsrc_row = We + (uint64_t)wrow(rw_row) * a.rb;
+
+    f32x16_t acc[4], inner[4];
 #pragma unroll
-                for (int i = 0; i < 8; i++) dst[i] = src[i];
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) dst[i] = make_uint4(0, 0, 0, 0);
-            }
-            if (part < 2) {
-                const uint32_t g0 = part * 4;
-#pragma unroll
-                for (int gg = 0; gg < 4; gg++)
-                    L.dx[g0 + gg][xr_lane] =
-                        xrow >= 0 ? a.xd[(uint64_t)xrow * (a.K / 32) + st * 8 + g0 + gg] : 0.f;
-            }
-        }
-        // weights: 64 rows x 8 groups = 512 group decodes, 2 per thread
-        for (uint32_t it = tid; it < NTW * 8; it += 256) {
-            const uint32_t r = it >> 3, j = it & 7u;
-            if (TY == Q4MI_T_IQ3_S) {
-                const uint8_t *blk = W + (uint64_t)r * a.rb + (uint64_t)st * IQ3S_BYTES;
-                iq3s_group_f16(L, blk, j, &L.w[r][32 * j]);
-                if (j == 0) L.dwb[r] = q4mi_h2f(ld_u16(blk));
-            } else {
-                const uint8_t *blk = W + (uint64_t)r * a.rb + (uint64_t)(st * 8 + j) * Q80_BYTES;
-                uint4 out[4];
-                uint32_t *o = (uint32_t *)out;
-#pragma unroll
-                for (int k = 0; k < 16; k++) {
-                    const uint32_t pr = ld_u16(blk + 2 + 2 * k);
-                    const _Float16 lo = (_Float16)(float)(int8_t)(pr & 0xffu);
-                    const _Float16 hi = (_Float16)(float)(int8_t)(pr >> 8);
-                    o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
-                           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-                }
-                uint4 *d4 = (uint4 *)&L.w[r][32 * j];
-#pragma unroll
-                for (int i = 0; i < 4; i++) d4[i] = out[i];
-                L.dwg[j][r] = q4mi_h2f(ld_u16(blk));
-            }
-        }
+    for (int t = 0; t < 4; t++) {
+        acc[t] = f32x16_t{};
+        inner[t] = f32x16_t{};
+    }
+    const uint32_t arow = 32 * wv + (lane & 31u);    // this lane's weight row in the tile
+    const uint32_t nsb = a.K / 256;
+    for (uint32_t sbi = 0; sbi < nsb; sbi++) {
         __syncthreads();
-        const uint32_t kb = (lane >> 5) * 8;   // this lane's 8-value k slice
-        const uint32_t rw_ = wn * 32 + (lane & 31u);
-        const uint32_t rx = wm * 32 + (lane & 31u);
+        {   // raw weight bytes of superblock sbi for row rw_row
+            const uint8_t *src = wsrc_row + (uint64_t)sbi * SB;
+            const uintptr_t a0 = (uintptr_t)src & ~(uintptr_t)3;
+            const uint32_t nd = (uint32_t)(((uintptr_t)src + SB + 3 - a0) / 4);
+            uint32_t *dst = (uint32_t *)&L.raw[rw_row][0];
+            const uint32_t *s32 = (const uint32_t *)a0;
+            for (uint32_t i = rw_part; i < nd; i += 2) dst[i] = s32[i];
+            if (rw_part == 0) {
+                if (TY == Q4MI_T_IQ3_S) {
+                    L.dwb[rw_row] = q4mi_h2f(*(const uint16_t *)src);
+                } else {
 #pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const half8_t A0 = *(const half8_t *)&L.w[rw_][32 * g + kb];
-            const half8_t B0 = *(const half8_t *)&L.x[rx][32 * g + kb];
-            const half8_t A1 = *(const half8_t *)&L.w[rw_][32 * g + 16 + kb];
-            const half8_t B1 = *(const half8_t *)&L.x[rx][32 * g + 16 + kb];
-            f32x16_t s = {};
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, s, 0, 0, 0);
-            const float dxv = L.dx[g][rx];
-            if (TY == Q4MI_T_IQ3_S) {
+                    for (int j = 0; j < 8; j++)
+                        L.dwg[j][rw_row] = q4mi_h2f(*(const uint16_t *)(src + 34 * j));
+                }
+            }
+        }
+        for (uint32_t half = 0; half < 2; half++) {
+            if (half) __syncthreads();
+            {   // activation codes: K values [sbi*256 + half*128, +128) of 128 rows
+                uint4 *dst = (uint4 *)&L.act[st_row][st_half * 64];
+                if (xrow >= 0) {
+                    const uint4 *src = (const uint4 *)(a.xq + (uint64_t)xrow * a.K + sbi * 256 +
+                                                       half * 128 + st_half * 64);
 #pragma unroll
-                for (int i = 0; i < 16; i++) inner[i] = fmaf(s[i], dxv, inner[i]);
-            } else {
+                    for (int i = 0; i < 8; i++) dst[i] = src[i];
+                    if (st_half == 0) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const uint32_t n = wn * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i % 4);
-                    acc[i] = fmaf(s[i], dxv * L.dwg[g][n], acc[i]);
+                        for (int g = 0; g < 4; g++)
+                            L.dx[g][st_row] =
+                                a.xd[(uint64_t)xrow * (a.K / 32) + sbi * 8 + half * 4 + g];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) dst[i] = make_uint4(0, 0, 0, 0);
+                    if (st_half == 0) {
+#pragma unroll
+                        for (int g = 0; g < 4; g++) L.dx[g][st_row] = 0.f;
+                    }
+                }
+            }
+            __syncthreads();
+            // the row's raw bytes start at the same offset inside its slot as
+            // in memory (the slot begins at the enclosing dword)
+            const uint32_t roff =
+                (uint32_t)(((uintptr_t)(We + (uint64_t)wrow(arow) * a.rb + (uint64_t)sbi * SB)) & 3);
+            const uint8_t *R = &L.raw[arow][roff];
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) {
+                const uint32_t j = half * 4 + gg;    // group inside the superblock
+                half8_t A0, A1;
+                decode_a<TY>(L, R, j, kh, A0, A1);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    if ((uint32_t)t < nts) {
+                        const uint32_t tok = 32 * t + (lane & 31u);
+                        const half8_t B0 = *(const half8_t *)&L.act[tok][32 * gg + 8 * kh];
+                        const half8_t B1 = *(const half8_t *)&L.act[tok][32 * gg + 16 + 8 * kh];
+                        f32x16_t sacc = {};
+                        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, sacc, 0, 0, 0);
+                        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, sacc, 0, 0, 0);
+                        const float dxv = L.dx[gg][tok];
+                        if (TY == Q4MI_T_IQ3_S) {
+#pragma unroll
+                            for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 16; i++) {
+                                const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
+                                acc[t][i] = fmaf(sacc[i], dxv * L.dwg[j][n], acc[t][i]);
+                            }
+                        }
+                    }
                 }
             }
         }
         if (TY == Q4MI_T_IQ3_S) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const uint32_t n = wn * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i % 4);
-                acc[i] = fmaf(inner[i], L.dwb[n], acc[i]);
-                inner[i] = 0.f;
+                const float dw = L.dwb[32 * wv + 8 * (i / 4) + 4 * kh + (i % 4)];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    acc[t][i] = fmaf(inner[t][i], dw, acc[t][i]);
+                    inner[t][i] = 0.f;
+                }
             }
         }
     }
-    // write: lane holds token column p = wm*32 + lane%32 and 16 weight rows
-    const uint32_t p = wm * 32 + (lane & 31u);
-    if (p < mrows) {
-        float *o = a.dst + (uint64_t)(rbase + (int32_t)p) * a.ld + n0 + wn * 32 + 4 * (lane >> 5);
+    if (!FUSED) {
+        // lane: token column 32t + lane%32, weight rows 32wv + 8b + 4kh + 0..3
 #pragma unroll
-        for (int b = 0; b < 4; b++)
-            *(float4 *)(o + 8 * b) =
-                make_float4(acc[4 * b], acc[4 * b + 1], acc[4 * b + 2], acc[4 * b + 3]);
+        for (int t = 0; t < 4; t++) {
+            const uint32_t p = 32 * t + (lane & 31u);
+            if (p < mrows) {
+                float *o = a.dst + (uint64_t)(rbase + (int32_t)p) * a.ld + nblk + 32 * wv + 4 * kh;
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    *(float4 *)(o + 8 * b) = make_float4(acc[t][4 * b], acc[t][4 * b + 1],
+                                                         acc[t][4 * b + 2], acc[t][4 * b + 3]);
+            }
+        }
+        return;
+    }
+    // fused: waves 2,3 (up rows) hand their accumulators to waves 0,1
+    __syncthreads();
+    float *ex = (float *)&L.act[0][0];   // [2 waves][4 t][16 i][64 lanes]
+    if (wv >= 2) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) ex[(((wv - 2) * 4 + t) * 16 + i) * 64 + lane] = acc[t][i];
+    }
+    __syncthreads();
+    if (wv >= 2) return;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t p = 32 * t + (lane & 31u);
+        float h[16];
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float g = acc[t][i];
+            const float u = ex[((wv * 4 + t) * 16 + i) * 64 + lane];
+            h[i] = g / (1.f + expf(-g)) * u;
+            amax = fmaxf(amax, fabsf(h[i]));
+        }
+        // the q8 group = h columns 32wv + 0..31 of token p: this lane has
+        // columns 8b + 4kh + 0..3, the partner lane (lane ^ 32) the rest
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const float d = __fdiv_rn(amax, 127.f);
+        const float sc = amax > 0.f ? __fdiv_rn(127.f, amax) : 0.f;
+        if (p < mrows) {
+            const uint64_t prow = (uint64_t)(rbase + (int32_t)p);
+            _Float16 *o = a.hq + prow * a.n_ff + nblk + 32 * wv + 4 * kh;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                half4_t v;
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[c] = (_Float16)(float)q4mi_q8_code(h[4 * b + c] * sc);
+                *(half4_t *)(o + 8 * b) = v;
+            }
+            if (kh == 0) a.hd[prow * (a.n_ff / 32) + (nblk + 32 * wv) / 32] = d;
+        }
     }
 }
 
@@ -315,7 +434,7 @@ static bool ensure_tiles(uint32_t n) {
 
 bool mmq_supported(uint32_t ty, uint64_t w_rows, uint64_t w_cols) {
     if (ty != Q4MI_T_IQ3_S && ty != Q4MI_T_Q8_0) return false;
-    return w_rows > 0 && w_rows % NTW == 0 && w_cols > 0 && w_cols % KS == 0 &&
+    return w_rows > 0 && w_rows % MMQ_NB == 0 && w_cols > 0 && w_cols % 256 == 0 &&
            w_cols <= 65536;
 }
 
@@ -329,12 +448,40 @@ bool mmq_quant(const float *x, const int32_t *ids, void *xq, uint64_t cols, uint
     return launch_ok("mmq_quant_k");
 }
 
-// xq rows = xrows (activation rows); act_row maps packed rows to them.
+template <uint32_t TY, bool FUSED>
+static bool set_lds_attr() {
+    static bool done = false;
+    if (done) return true;
+    if (hipFuncSetAttribute((const void *)mmq_k<TY, FUSED>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(MmqLds<TY>)) != hipSuccess) {
+        set_error("mmq: cannot raise the LDS limit to %zu bytes", sizeof(MmqLds<TY>));
+        return false;
+    }
+    done = true;
+    return true;
+}
+
+template <uint32_t TY, bool FUSED>
+static bool mmq_launch(const MmqArgs &a, dim3 grid) {
+    if (!set_lds_attr<TY, FUSED>()) return false;
+    mmq_k<TY, FUSED><<<grid, dim3(256), sizeof(MmqLds<TY>), stream()>>>(a);
+    return launch_ok("mmq_k");
+}
+
+// xq holds xrows activation rows; act_row (optional) maps packed row p to
+// its activation row.  Plain mode writes dst[p][0..w_rows); fused mode
+// (w_rows = 2*n_ff, gate rows then up rows) writes the q8 codes of
+// h = silu(gate)*up into hq (the q4_mmq_q8_bytes(total_rows, n_ff) layout).
 bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, uint64_t estride,
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
-             const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld) {
+             const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq) {
     if (!total_rows) return true;
     const uint32_t max_tiles = (uint32_t)(total_rows / MT + n_exp + 1);
+    if (max_tiles > 65535) {
+        set_error("mmq: too many row tiles (%u)", max_tiles);
+        return false;
+    }
     if (!ensure_tiles(max_tiles)) {
         set_error("mmq: tile buffer allocation failed");
         return false;
@@ -346,7 +493,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.estride = estride;
     a.rb = (uint32_t)q4mi_row_bytes(ty, w_cols);
     a.K = (uint32_t)w_cols;
-    a.N = (uint32_t)w_rows;
+    a.n_ff = (uint32_t)(w_rows / 2);
     a.xq = (const _Float16 *)xq;
     a.xd = (const float *)((const uint8_t *)xq + xrows * w_cols * 2);
     a.act_row = act_row;
@@ -355,25 +502,16 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.ntiles = g_ntiles;
     a.dst = dst;
     a.ld = ld;
-    const dim3 grid((uint32_t)(w_rows / NTW), max_tiles);
-    const size_t lds = sizeof(Fp16Lds);
-    static bool attr = false;
-    if (!attr) {
-        // the tile needs more than the default 64 KiB of dynamic LDS
-        if (hipFuncSetAttribute((const void *)mmq_k<Q4MI_T_IQ3_S>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess ||
-            hipFuncSetAttribute((const void *)mmq_k<Q4MI_T_Q8_0>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            set_error("mmq: cannot raise the LDS limit to %zu bytes", lds);
-            return false;
-        }
-        attr = true;
+    a.hq = (_Float16 *)hq;
+    a.hd = hq ? (float *)((uint8_t *)hq + total_rows * a.n_ff * 2) : nullptr;
+    if (hq) {
+        const dim3 grid((uint32_t)(a.n_ff / 64), max_tiles);
+        return ty == Q4MI_T_IQ3_S ? mmq_launch<Q4MI_T_IQ3_S, true>(a, grid)
+                                  : mmq_launch<Q4MI_T_Q8_0, true>(a, grid);
     }
-    if (ty == Q4MI_T_IQ3_S)
-        mmq_k<Q4MI_T_IQ3_S><<<grid, dim3(256), lds, stream()>>>(a);
-    else
-        mmq_k<Q4MI_T_Q8_0><<<grid, dim3(256), lds, stream()>>>(a);
-    return launch_ok("mmq_k");
+    const dim3 grid((uint32_t)(w_rows / MMQ_NB), max_tiles);
+    return ty == Q4MI_T_IQ3_S ? mmq_launch<Q4MI_T_IQ3_S, false>(a, grid)
+                              : mmq_launch<Q4MI_T_Q8_0, false>(a, grid);
 }
 
 bool swiglu_launch(const float *gu, float *h, uint64_t rows, uint64_t n_ff) {
@@ -413,9 +551,9 @@ uint32_t q4_mmq_group(void) {
     return (uint32_t)v;
 }
 
-/* A tile exists for (type, w_rows): IQ3_S or Q8_0, w_rows % 64 == 0. */
+/* A tile exists for (type, w_rows): IQ3_S or Q8_0, w_rows % 128 == 0. */
 bool q4_mmq_supported(uint32_t type, uint64_t w_rows) {
-    return (type == Q4MI_T_IQ3_S || type == Q4MI_T_Q8_0) && w_rows > 0 && w_rows % NTW == 0;
+    return (type == Q4MI_T_IQ3_S || type == Q4MI_T_Q8_0) && w_rows > 0 && w_rows % MMQ_NB == 0;
 }
 
 /* Bytes of the activation buffer q4_mmq_quantize fills for rows x cols:
@@ -453,7 +591,51 @@ bool q4_mmq_mul_id(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_col
         return false;
     }
     return mmq_run((const uint8_t *)w, type, w_rows, w_cols, expert_stride_bytes, n_expert, xq,
-                   total_rows, nullptr, bounds, total_rows, dst, ld_dst);
+                   total_rows, nullptr, bounds, total_rows, dst, ld_dst, nullptr);
+}
+
+/* q4_mmq_mul_id with the activation rows gathered through act_row: xq
+ * holds xrows rows (e.g. one per token, quantized once) and packed row p
+ * reads xq row act_row[p] (e.g. the pack's a_tok).  No reference
+ * counterpart: it removes the gathered q8 copy of every routed row. */
+bool q4mi_mmq_mul_id_rows(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_cols,
+                          uint64_t expert_stride_bytes, uint32_t n_expert, const void *xq,
+                          uint64_t xrows, const int32_t *act_row, const int32_t *bounds,
+                          uint64_t total_rows, float *dst, uint64_t ld_dst) {
+    if (!w || !xq || !bounds || !dst || !n_expert || n_expert > 512 || !w_cols || !ld_dst ||
+        ld_dst % 4 || ((uintptr_t)dst & 15) || ((uintptr_t)xq & 15) || !xrows) {
+        set_error("q4mi_mmq_mul_id_rows: bad arguments");
+        return false;
+    }
+    if (!mmq_supported(type, w_rows, w_cols)) {
+        set_error("q4mi_mmq_mul_id_rows: type/shape not covered");
+        return false;
+    }
+    return mmq_run((const uint8_t *)w, type, w_rows, w_cols, expert_stride_bytes, n_expert, xq,
+                   xrows, act_row, bounds, total_rows, dst, ld_dst, nullptr);
+}
+
+/* Fused gate/up MMQ: each expert's 2*n_ff x w_cols matrix (gate rows then
+ * up rows) against xq rows (gathered through act_row when given); writes the
+ * q8 of h = silu(gate)*up straight into hq, the q4_mmq_q8_bytes(total_rows,
+ * n_ff) activation buffer the down q4_mmq_mul_id reads.  Replaces the
+ * reference's mul_id(gate|up) + q4_mmq_swiglu + q4_mmq_quantize(h) sequence
+ * (src/q4_moe.c:3718-3730) with one launch. */
+bool q4mi_mmq_gate_up(const void *w, uint32_t type, uint64_t n_ff, uint64_t w_cols,
+                      uint64_t expert_stride_bytes, uint32_t n_expert, const void *xq,
+                      uint64_t xrows, const int32_t *act_row, const int32_t *bounds,
+                      uint64_t total_rows, void *hq) {
+    if (!w || !xq || !bounds || !hq || !n_expert || n_expert > 512 || !w_cols || !xrows ||
+        ((uintptr_t)hq & 15) || ((uintptr_t)xq & 15) || n_ff % 64) {
+        set_error("q4mi_mmq_gate_up: bad arguments");
+        return false;
+    }
+    if (!mmq_supported(type, 2 * n_ff, w_cols)) {
+        set_error("q4mi_mmq_gate_up: type/shape not covered");
+        return false;
+    }
+    return mmq_run((const uint8_t *)w, type, 2 * n_ff, w_cols, expert_stride_bytes, n_expert,
+                   xq, xrows, act_row, bounds, total_rows, nullptr, 0, hq);
 }
 
 /* h[r][k] = silu(gu[r][k]) * gu[r][n_ff + k]. */

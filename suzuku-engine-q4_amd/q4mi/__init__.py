@@ -64,6 +64,10 @@ _SIGS = {
     "q4_mmq_quantize": (_b, [_vp, _vp, _vp, _u32, _u64, _u64]),
     "q4_mmq_mul_id": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _vp, _u32, _u64, _vp, _u64]),
     "q4_mmq_swiglu": (_b, [_vp, _vp, _u64, _u64]),
+    "q4mi_mmq_mul_id_rows": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp, _u64,
+                                  _vp, _u64]),
+    "q4mi_mmq_gate_up": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp, _u64,
+                              _vp]),
 }
 
 _lib = None
