@@ -1,26 +1,38 @@
 // Routed-expert decode (1 token) and verify window (2..8 tokens) over
 // IQ3_S / Q8_0 experts resident at base + slot*stride.
 //
-// Two persistent launches per layer, one 512-thread block per CU:
+// Two launches per layer, one 1024-thread block per CU:
 //   moe_gu_k  the (unique expert u, intermediate row r) pairs are split into
-//             one contiguous share per block; the share's gate and up rows
-//             stream HBM -> LDS (global_load_lds) in double-buffered chunks,
-//             the next chunk in flight while the current one is computed, and
-//             h[u][t][r] = silu(gate_r . q8(x_t)) * (up_r . q8(x_t)).
+//             one contiguous share per block; h[u][t][r] =
+//             silu(gate_r . q8(x_t)) * (up_r . q8(x_t)) goes out as fp32.
 //   moe_dn_k  each block owns 8 output rows: it quantizes every selected
-//             h[u][t] into LDS, dots its rows of every expert's down matrix,
-//             and adds sum_u w[u][t] * pd[u][t][r] into y[t][r] in
-//             unique-expert order -- deterministic, no atomics.
+//             h[u][t] (q8, 32-value groups) into LDS, dots its rows of every
+//             expert's down matrix and writes y[t][r] += sum_u w[u][t] *
+//             part[u][t][r] in unique-expert order -- deterministic, no atomics.
 // Each unique expert's rows are read once per launch and dotted with every
 // token that selected it (the verify window's reuse; reference
 // q4_hip_moe_exec_win src/q4_rocm.cu:7444-7531, CPU twin
 // q4_cpuex_dispatch_win src/q4_cpuexp.c:2618-2753).
 //
+// Memory pipeline (both kernels): every byte a block needs is copied
+// HBM -> LDS with gfx950 global_load_lds (no registers).  A prologue copies
+// the small inputs (IQ3_S code table, x or h, y), then the block's weight
+// rows are issued as up to S chunks into an LDS ring before anything waits.
+// VMEM loads of a wave complete in issue order, so a wave waits for chunk c
+// with s_waitcnt vmcnt(#loads it issued after chunk c) and a plain s_barrier
+// makes every wave's part visible: chunk c is computed while chunks c+1..
+// are still in flight, and no wait ever covers more than it needs.
+//
 // IQ3_S decode: one LDS lookup per 4 values into an 8192-entry table of
-// signed int8 quads indexed by (sign nibble, qh bit, qs byte), one
-// v_dot4_i32_i8 per quad per token, the (2s+1) multiplier on the exact int32
-// group sum, then float(S) * (d_w * d_x).
+// signed int8 quads (index = sign nibble << 9 | qh bit << 8 | qs byte), built
+// in LDS from the 512-entry codebook at kernel start.  The index of quad k
+// is one v_perm_b32 of the qs bytes with a per-group byte vector of
+// (sign nibble << 1 | qh bit); then v_dot4_i32_i8 per quad and token, the
+// (2s+1) multiplier on the exact int32 group sum, and float(S) * (d_w * d_x).
+#include <stddef.h>
 #include <stdlib.h>
+
+#include <algorithm>
 
 #include "mmvq_engine.h"
 #include "q4mi_internal.h"
@@ -29,8 +41,15 @@ namespace q4mi {
 
 constexpr uint32_t kMaxU = 64;    // unique experts per call (reference bound n<=64)
 constexpr uint32_t kMaxT = 8;     // tokens per call
-constexpr uint32_t kThreads = 1024;
+constexpr uint32_t kT = 1024;     // threads per block
+#ifndef Q4MI_PROD
+#define Q4MI_PROD 4
+#endif
+constexpr uint32_t kProd = Q4MI_PROD;   // producer waves (issue the LDS copies)
+constexpr uint32_t kCons = kT - kProd * 64;   // consumer threads
+constexpr uint32_t kConsW = kCons / 64;       // consumer waves
 constexpr uint32_t kDnRows = 8;   // output rows per down block
+constexpr uint32_t kMaxS = 16;    // LDS ring slots
 
 struct HostList {
     int32_t id[kMaxU];
@@ -53,39 +72,14 @@ struct __align__(16) Plan {
     int32_t uid[kMaxU];
     uint32_t sel[kMaxU];            // token bitmask per unique expert
     uint32_t pslot[kMaxU];          // first pair slot of u (slots in (u, t) order)
-    float w[kMaxU][kMaxT];
+    uint32_t prow[kMaxU];           // pair slot -> h row u * kMaxT + t
+    float w[kMaxT][kMaxU];          // routing weight of (token, unique expert)
+    uint32_t ends[kProd][kMaxS];    // per producer: copies issued up to the end of a ring chunk
 };
 
-// Wave 0 builds the plan (first-appearance order over (token, pick));
-// callers sync afterwards.
-__device__ void build_plan(Plan *P, const ListSrc &s, const HostList &hl, uint32_t lane) {
-    if (s.unique) {   // deduplicated on the host: the plan is the list itself
-        const uint32_t nu = s.n_fixed;
-        // uniform loop: the kernel-argument list is read with scalar loads
-        for (uint32_t u = 0; u < nu; u++) {
-            const int32_t id = hl.id[u];
-            const float w = hl.w[u];
-            if (lane == 0) {
-                P->uid[u] = id;
-                P->w[u][0] = w;
-            }
-        }
-        if (lane < kMaxU) {
-            P->sel[lane] = lane < nu ? 1u : 0u;
-            P->pslot[lane] = lane;
-#pragma unroll
-            for (uint32_t t = 1; t < kMaxT; t++) P->w[lane][t] = 0.f;
-            if (lane >= nu) {
-                P->uid[lane] = -1;
-                P->w[lane][0] = 0.f;
-            }
-        }
-        if (lane == 0) {
-            P->nu = nu;
-            P->nsel = nu;
-        }
-        return;
-    }
+// Device lists: wave 0 builds the plan (first-appearance order over
+// (token, pick)); callers sync afterwards.
+__device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
     // lane -> (token, pick) of the flattened lists, token-major
     uint32_t E = 0, tok = 0, rem = 0;
     bool found = false;
@@ -104,13 +98,8 @@ __device__ void build_plan(Plan *P, const ListSrc &s, const HostList &hl, uint32
     int32_t id = -1;
     float w = 0.f;
     if (lane < E) {
-        if (s.es) {
-            id = s.es[(size_t)tok * s.stride + rem];
-            w = s.ew[(size_t)tok * s.stride + rem];
-        } else {
-            id = hl.id[rem];
-            w = hl.w[rem];
-        }
+        id = s.es[(size_t)tok * s.stride + rem];
+        w = s.ew[(size_t)tok * s.stride + rem];
     }
     const bool valid = lane < E && id >= 0;
     uint32_t first_j = lane;
@@ -124,8 +113,9 @@ __device__ void build_plan(Plan *P, const ListSrc &s, const HostList &hl, uint32
     const uint32_t u = (uint32_t)__popcll(fm & ((1ull << first_j) - 1ull));
     for (uint32_t i = lane; i < kMaxU; i += 64) {
         P->sel[i] = 0;
+        P->uid[i] = -1;
 #pragma unroll
-        for (uint32_t t = 0; t < kMaxT; t++) P->w[i][t] = 0.f;
+        for (uint32_t t = 0; t < kMaxT; t++) P->w[t][i] = 0.f;
     }
     const uint32_t nu = (uint32_t)__popcll(fm);
     if (lane == 0) P->nu = nu;
@@ -134,7 +124,7 @@ __device__ void build_plan(Plan *P, const ListSrc &s, const HostList &hl, uint32
     if (first) P->uid[u] = id;
     if (valid) {
         atomicOr(&P->sel[u], 1u << tok);
-        P->w[u][tok] = w;
+        P->w[tok][u] = w;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
@@ -146,8 +136,152 @@ __device__ void build_plan(Plan *P, const ListSrc &s, const HostList &hl, uint32
         const uint32_t v = __shfl_up(incl, o);
         if (lane >= (uint32_t)o) incl += v;
     }
-    if (lane < nu) P->pslot[lane] = incl - c;
+    if (lane < nu) {
+        P->pslot[lane] = incl - c;
+        uint32_t k = incl - c;
+        const uint32_t sl = P->sel[lane];
+        for (uint32_t t = 0; t < kMaxT; t++)
+            if ((sl >> t) & 1u) P->prow[k++] = lane * kMaxT + t;
+    }
     if (lane == 63) P->nsel = incl;
+}
+
+// ------------------------------------------------------------ LDS pipeline
+// Wait until at most n VMEM operations of this wave are outstanding.  The
+// count is an instruction immediate, so a runtime n selects among literal
+// waits; n beyond the 6-bit field waits for more than asked, never less.
+__device__ inline void wait_vm(uint32_t n) {
+    switch (__builtin_amdgcn_readfirstlane(n)) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+    case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+    case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+    case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+    case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+    case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+    case 33: asm volatile("s_waitcnt vmcnt(33)" ::: "memory"); break;
+    case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
+    case 35: asm volatile("s_waitcnt vmcnt(35)" ::: "memory"); break;
+    case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
+    case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
+    case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
+    case 39: asm volatile("s_waitcnt vmcnt(39)" ::: "memory"); break;
+    case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
+    case 41: asm volatile("s_waitcnt vmcnt(41)" ::: "memory"); break;
+    case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
+    case 43: asm volatile("s_waitcnt vmcnt(43)" ::: "memory"); break;
+    case 44: asm volatile("s_waitcnt vmcnt(44)" ::: "memory"); break;
+    case 45: asm volatile("s_waitcnt vmcnt(45)" ::: "memory"); break;
+    case 46: asm volatile("s_waitcnt vmcnt(46)" ::: "memory"); break;
+    case 47: asm volatile("s_waitcnt vmcnt(47)" ::: "memory"); break;
+    case 48: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
+    case 49: asm volatile("s_waitcnt vmcnt(49)" ::: "memory"); break;
+    case 50: asm volatile("s_waitcnt vmcnt(50)" ::: "memory"); break;
+    case 51: asm volatile("s_waitcnt vmcnt(51)" ::: "memory"); break;
+    case 52: asm volatile("s_waitcnt vmcnt(52)" ::: "memory"); break;
+    case 53: asm volatile("s_waitcnt vmcnt(53)" ::: "memory"); break;
+    case 54: asm volatile("s_waitcnt vmcnt(54)" ::: "memory"); break;
+    case 55: asm volatile("s_waitcnt vmcnt(55)" ::: "memory"); break;
+    case 56: asm volatile("s_waitcnt vmcnt(56)" ::: "memory"); break;
+    case 57: asm volatile("s_waitcnt vmcnt(57)" ::: "memory"); break;
+    case 58: asm volatile("s_waitcnt vmcnt(58)" ::: "memory"); break;
+    case 59: asm volatile("s_waitcnt vmcnt(59)" ::: "memory"); break;
+    case 60: asm volatile("s_waitcnt vmcnt(60)" ::: "memory"); break;
+    case 61: asm volatile("s_waitcnt vmcnt(61)" ::: "memory"); break;
+    case 62: asm volatile("s_waitcnt vmcnt(62)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
+    }
+}
+
+// Workgroup barrier without the compiler's fence: LDS ops of this wave are
+// complete (lgkmcnt) but outstanding VMEM copies are left in flight.
+__device__ inline void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One global -> LDS wave copy (gfx950 global_load_lds): lane i's UNIT bytes
+// at g land at LDS byte address m0 + i*UNIT.  Written as inline asm so that
+// the compiler does not track it: its own tracking of LDS copies waits for
+// all of them (vmcnt(0)) before any later LDS read, which would serialize
+// the pipeline.  Completion is this library's business: wait_vm + bar.
+template <uint32_t UNIT>
+__device__ inline void lds_copy(const void *g, uint32_t lds_addr) {
+    lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+    if constexpr (UNIT == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :: "v"(g), "s"(lds_addr) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                     :: "v"(g), "s"(lds_addr) : "memory", "m0");
+}
+
+__device__ inline uint32_t lds_addr_of(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+// Asynchronous copy of `bytes` (a multiple of UNIT, both ends UNIT-aligned)
+// global -> LDS by the calling wave, in operations of 64*UNIT bytes.
+// Returns the number of operations issued.
+template <uint32_t UNIT>
+__device__ inline uint32_t dma1(uint8_t *dst, const uint8_t *src, uint32_t bytes, uint32_t lane) {
+    constexpr uint32_t OPB = 64 * UNIT;
+    const uint32_t nops = (bytes + OPB - 1) / OPB;
+    const uint32_t l0 = lds_addr_of(dst);
+    for (uint32_t j = 0; j < nops; j++) {
+        const uint32_t off = j * OPB + lane * UNIT;
+        if (off < bytes) lds_copy<UNIT>(src + off, l0 + j * OPB);
+    }
+    return nops;
+}
+
+// Signed IQ3_S table in LDS, built by the consumer threads from the
+// 512-entry codebook.
+// Thread ct < 512 owns codebook entry ct (`c`, loaded by the caller).
+__device__ inline void build_stab(uint32_t *stab, uint32_t c, uint32_t ct) {
+    static_assert(kCons >= 512, "one codebook entry per consumer thread");
+    if (ct < 512) {
+        const uint32_t i = ct;
+        uint32_t g = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) g |= (2u * ((c >> (3 * j)) & 7u) + 1u) << (8 * j);
+#pragma unroll
+        for (uint32_t s4 = 0; s4 < 16; s4++)
+            stab[(s4 << 9) | i] = (uint32_t)q4mi_sign4(g, q4mi_expand4(s4));
+    }
+}
+
+// q8 of quad i (values 4i..4i+3) of a run of 32-value groups: the 8 lanes
+// holding quads 8g..8g+7 quantize group g together (all 8 must be active).
+__device__ inline void quant_quad(float4 v, uint32_t i, int8_t *q, float *d) {
+    float dd;
+    int bs;
+    const uint32_t c = q4mi_quant_team8(v, &dd, &bs);
+    ((uint32_t *)q)[i] = c;
+    if ((i & 7u) == 0) d[i / 8] = dd;
 }
 
 // DPP reduction over aligned groups of W lanes (W = 8, 16, 32, 64); the
@@ -182,11 +316,18 @@ __device__ inline void iq3s_group(const uint32_t *stab, const uint8_t *lb, const
     const uint32_t sg = lds_u32_at(lw, B + 74u + 4u * j);
     const uint32_t sc = lb[B + 106u + (j >> 1)];
     mult = 2 * (int)((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1;
+    // byte k of hlo / hhi: (sign nibble << 1 | qh bit) of quad k / k+4
+    const uint32_t ne = sg & 0x0F0F0F0Fu, no = (sg >> 4) & 0x0F0F0F0Fu;
+    const uint32_t slo = __builtin_amdgcn_perm(no, ne, 0x05010400u);
+    const uint32_t shi = __builtin_amdgcn_perm(no, ne, 0x07030602u);
+    const uint32_t blo = __umul24(qh & 15u, 0x00204081u) & 0x01010101u;
+    const uint32_t bhi = __umul24(qh >> 4, 0x00204081u) & 0x01010101u;
+    const uint32_t hlo = (slo << 1) | blo, hhi = (shi << 1) | bhi;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        const uint32_t qb = __builtin_amdgcn_ubfe(k < 4 ? q0 : q1, 8 * (k & 3), 8);
-        const uint32_t hs = (__builtin_amdgcn_ubfe(sg, 4 * k, 4) << 1) | __builtin_amdgcn_ubfe(qh, k, 1);
-        w[k] = (int32_t)stab[qb | (hs << 8)];
+        const uint32_t sel = 0x0C0C0000u | ((4u + (k & 3)) << 8) | (uint32_t)(k & 3);
+        const uint32_t idx = __builtin_amdgcn_perm(k < 4 ? hlo : hhi, k < 4 ? q0 : q1, sel);
+        w[k] = (int32_t)stab[idx];
     }
 }
 
@@ -222,133 +363,247 @@ struct MoeArgs {
     uint32_t n_embd;
     uint32_t rb_gu, rb_dn;
     uint32_t chunk;   // gate/up: pairs per chunk; down: experts per chunk
+    uint32_t slots;   // LDS ring slots (<= kMaxS)
+    uint32_t nsel_cap;  // down: q8(h) rows the LDS holds
     const float *x;   // [n_tok][K]
-    int8_t *hq;       // [kMaxU][kMaxT][n_ff] q8 codes of h
-    float *hd;        // [kMaxU][kMaxT][n_ff/32] their scales
+    float *h;         // [kMaxU][kMaxT][n_ff] fp32 h
     float *y;         // [n_tok][n_embd], accumulated
-    const uint32_t *stab;   // signed IQ3_S table (device)
     ListSrc src;
-    uint32_t dbg;     // Q4MI_DBG phase-skip mask (measurement only; 0 = normal)
+#ifdef Q4MI_TRACE
+    unsigned long long *trace;   // [2 kernels][4096 blocks][32] phase timestamps
+#endif
+    HostList hl;      // host list (src.unique), read in place from the kernel arguments
 };
+
+// Optional build (-DQ4MI_TRACE): the first producer and the first consumer
+// thread of every block record wall-clock phase timestamps (10 ns ticks).
+#ifdef Q4MI_TRACE
+#define Q4MI_TR_DECL unsigned long long *const q4tr = a.trace
+#define Q4MI_TR(k, kern, who) do { if (q4tr && (who)) q4tr[((size_t)(kern) * 4096 + blockIdx.x) * 32 + (k)] = wall_clock64(); } while (0)
+#else
+#define Q4MI_TR_DECL do { } while (0)
+#define Q4MI_TR(k, kern, who) do { } while (0)
+#endif
+
+// The kernel's own argument block (kernel parameters start at offset 0 of
+// the kernarg segment).  Uniform reads through it are scalar loads, and the
+// host list can be copied from it into LDS like any other global bytes.
+typedef const __attribute__((address_space(4))) MoeArgs *KArgs;
+__device__ inline KArgs kargs() { return (KArgs)__builtin_amdgcn_kernarg_segment_ptr(); }
+
+// The host list's ids, one per lane (lane u holds id u), gathered with
+// constant-offset scalar loads (a vector load of the kernel arguments costs
+// a full memory round trip at kernel start).
+typedef const __attribute__((address_space(4))) int32_t *KWords;
+
+template <int K>
+__device__ inline int32_t put_lane(int32_t v, int32_t s) {
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(s), "i"(K));
+    return v;
+}
+// Words [16B, 16B + 16) of w into lanes 16B.. of v: sixteen constant-offset
+// scalar loads (merged into wide loads) and sixteen v_writelane.
+template <int B>
+__device__ inline int32_t put16(int32_t v, KWords w) {
+    int32_t s[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) s[k] = w[16 * B + k];
+    v = put_lane<16 * B + 0>(v, s[0]);   v = put_lane<16 * B + 1>(v, s[1]);
+    v = put_lane<16 * B + 2>(v, s[2]);   v = put_lane<16 * B + 3>(v, s[3]);
+    v = put_lane<16 * B + 4>(v, s[4]);   v = put_lane<16 * B + 5>(v, s[5]);
+    v = put_lane<16 * B + 6>(v, s[6]);   v = put_lane<16 * B + 7>(v, s[7]);
+    v = put_lane<16 * B + 8>(v, s[8]);   v = put_lane<16 * B + 9>(v, s[9]);
+    v = put_lane<16 * B + 10>(v, s[10]); v = put_lane<16 * B + 11>(v, s[11]);
+    v = put_lane<16 * B + 12>(v, s[12]); v = put_lane<16 * B + 13>(v, s[13]);
+    v = put_lane<16 * B + 14>(v, s[14]); v = put_lane<16 * B + 15>(v, s[15]);
+    return v;
+}
+// The first n words of w, word k in lane k (entries beyond n keep `fill`).
+__device__ inline int32_t host_words(KWords w, uint32_t n, int32_t fill) {
+    int32_t v = fill;
+    v = put16<0>(v, w);
+    if (n > 16) v = put16<1>(v, w);
+    if (n > 32) v = put16<2>(v, w);
+    if (n > 48) v = put16<3>(v, w);
+    return v;
+}
+__device__ inline int32_t host_ids(KArgs ka, uint32_t n) { return host_words(ka->hl.id, n, -1); }
+__device__ inline float host_weights(KArgs ka, uint32_t n) {
+    return __builtin_bit_cast(float, host_words((KWords)ka->hl.w, n, 0));
+}
+
+
+__host__ __device__ inline size_t al16(size_t v) { return (v + 15) & ~(size_t)15; }
 
 __device__ inline float silu_f(float v) { return v / (1.f + expf(-v)); }
 
-// Asynchronous row staging, global -> LDS without registers (gfx950
-// global_load_lds): wave w copies rows w, w+8, ... of `nrows` rows of `rb`
-// bytes (row i from src(i)) to dst + i*rb, in UNIT-byte lanes (16 when
-// every row start and rb are 16-aligned, else 4).  The caller waits with
-// wait_stage() and a barrier before reading.
-template <uint32_t UNIT, class SrcFn>
-__device__ inline void stage_rows(uint8_t *dst, SrcFn src, uint32_t nrows, uint32_t rb,
-                                  uint32_t wave, uint32_t lane) {
-    const uint32_t units = rb / UNIT;
-    for (uint32_t r = wave; r < nrows; r += kThreads / 64) {
-        const uint8_t *sp = src(r);
-        uint8_t *dp = dst + (size_t)r * rb;
-        for (uint32_t u0 = 0; u0 < units; u0 += 64) {
-            if (u0 + lane < units) {
-                const void *g = (const void *)(sp + (size_t)(u0 + lane) * UNIT);
-                auto *l = (__attribute__((address_space(3))) void *)(dp + (size_t)u0 * UNIT);
-                if constexpr (UNIT == 16)
-                    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
-                else
-                    __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
-            }
-        }
-    }
+
+// ------------------------------------------------------------- pipeline sync
+// Producer waves never take part in a barrier (a copy issue stalls while
+// the memory system is saturated, and a stalled producer must not hold the
+// consumers back).  All hand-offs go through LDS counters instead:
+//   Sync::landed[p]  chunks of producer p that have landed (chunk c belongs
+//                    to producer c % kProd, landed in order)
+//   Sync::cons[s]    items finished in the chunk held by ring slot s
+//   Sync::ready      consumer waves done with the shared prologue work
+//   Sync::fin        consumer waves done with every item
+struct Sync {
+    uint32_t ready;
+    uint32_t fin;
+    uint32_t landed[kProd];
+    uint32_t cons[kMaxS];
+};
+
+__device__ inline uint32_t lds_ld(const uint32_t *p) { return *(const volatile uint32_t *)p; }
+__device__ inline void lds_st(uint32_t *p, uint32_t v) {
+    asm volatile("" ::: "memory");
+    *(volatile uint32_t *)p = v;
+}
+// Every wait is bounded: a block that would wait longer than about 0.1 s
+// gives up and runs on (its results are then wrong, which the parity tests
+// report), so a protocol error can never hang the device.
+constexpr uint32_t kSpinMax = 1u << 22;
+
+// Wait until *p >= v; later LDS reads stay after the poll.
+__device__ inline void spin_ge(const uint32_t *p, uint32_t v) {
+    for (uint32_t n = 0; lds_ld(p) < v && n < kSpinMax; n++) __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+}
+__device__ inline void wait_chunk(const Sync *y, uint32_t c) {
+    spin_ge(&y->landed[c % kProd], c / kProd + 1);
 }
 
-__device__ inline void wait_stage() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Asynchronous contiguous copy of `bytes` (multiple of 1024) global -> LDS.
-__device__ inline void dma_copy(uint8_t *dst, const uint8_t *src, uint32_t bytes, uint32_t wave,
-                                uint32_t lane) {
-    for (uint32_t o = wave * 1024; o < bytes; o += (kThreads / 64) * 1024)
-        __builtin_amdgcn_global_load_lds((const void *)(src + o + lane * 16),
-                                         (__attribute__((address_space(3))) void *)(dst + o), 16,
-                                         0, 0);
+// Producer side of the ring: chunks c = p, p + kProd, ... are issued while
+// their slot is free and published (landed[p]++) in order.  A slot is free
+// once the consumers finished every item of the chunk it held (cons[s]).
+// The producer never waits on a slot while one of its own issued chunks is
+// unpublished, so it cannot hold back a chunk the consumers are waiting for.
+template <class IssueFn, class ItemsFn, class TraceFn>
+__device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, uint32_t S,
+                               uint32_t &issued, IssueFn issue, ItemsFn items, TraceFn trace) {
+    uint32_t next = p, pub = p;    // next chunk to issue / to publish
+    auto slot_free = [&](uint32_t c) {
+        return c < S || lds_ld(&y->cons[c % S]) >= items(c - S);
+    };
+    uint32_t idle = 0;
+    while (pub < C && idle < kSpinMax) {
+        while (next < C && (next < pub + kProd * kMaxS) && slot_free(next)) {
+            if (next >= S) lds_st(&y->cons[next % S], 0);
+            issue(next);
+            ends[(next / kProd) % kMaxS] = issued;
+            next += kProd;
+        }
+        if (pub < next) {
+            wait_vm(issued - ends[(pub / kProd) % kMaxS]);
+            lds_st(&y->landed[p], pub / kProd + 1);
+            trace(pub);
+            pub += kProd;
+        } else {
+            __builtin_amdgcn_s_sleep(1);   // every own chunk published; wait for a slot
+            idle++;
+        }
+    }
+    wait_vm(0);
 }
 
 // ------------------------------------------------------------- gate / up
+// Roles: waves 0..kProd-1 produce (issue the weight copies global -> LDS),
+// the other waves consume (build the IQ3_S table, quantize x, compute).  The
+// block's share of (u, r) pairs is cut into chunks of `ch` pairs that flow
+// through a ring of S LDS slots; consumer team j (TPR lanes) computes pairs
+// j, j + teams, ... as soon as their chunk has landed.
+//
+// LDS: [stab 32 KB] (IQ3_S) Plan Sync | xq [NT][K] | xd [NT][K/32] | ring of
+//      S slots, slot = gate rows[ch] then up rows[ch].
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__global__ __launch_bounds__(kThreads) void moe_gu_k(MoeArgs a, HostList hl) {
+__global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint32_t *stab = (uint32_t *)smem;                              // 32 KB (IQ3_S)
-    Plan *P = (Plan *)(smem + (TY == Q4MI_T_IQ3_S ? 32768 : 0));
-    int8_t *xq = (int8_t *)(P + 1);
+    Q4MI_TR_DECL;
+    Q4MI_TR(31, 0, threadIdx.x == 0);
+    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
+    uint32_t *stab = (uint32_t *)smem;
+    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
+    Sync *Y = (Sync *)(P + 1);
+    int8_t *xq = (int8_t *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));
     float *xd = (float *)(xq + NT * a.K);
-    float *hbuf = xd + NT * (a.K / 32);               // [32][NT] h of the current unit
-    uint8_t *tile0 = (uint8_t *)(hbuf + 32 * NT);
-    uint8_t *tile1 = tile0 + (size_t)2 * a.chunk * a.rb_gu;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-    if (a.dbg & 256) {
-        if (tid < kMaxU) {
-            P->uid[tid] = tid;
-            P->sel[tid] = 1;
-            P->pslot[tid] = tid;
-            P->w[tid][0] = 0.1f;
-        }
-        if (tid == 0) P->nu = P->nsel = 11;
-    } else if (tid < 64) {
-        build_plan(P, a.src, hl, tid);
-    }
-    __syncthreads();
-    if (a.dbg & 512) return;
-    const uint32_t nt = a.src.n_tok;
-    const uint32_t nu = P->nu;
-    // shares are whole 32-row units (one q8 group of h per token)
-    const uint32_t U = nu * a.n_ff / 32;
-    const uint32_t p0 = 32u * (uint32_t)(((uint64_t)U * blockIdx.x) / gridDim.x);
-    const uint32_t p1 = 32u * (uint32_t)(((uint64_t)U * (blockIdx.x + 1)) / gridDim.x);
-    const uint32_t rb = a.rb_gu;
-    const uint32_t n_ff = a.n_ff;
-    const uint8_t *base = a.base;
-    const uint64_t stride = a.stride, og = a.og, ou = a.ou;
-    const int32_t *uid = P->uid;
-    auto src_of = [=](uint32_t pc0) {
-        return [=](uint32_t i) -> const uint8_t * {
-            const uint32_t p = pc0 + (i >> 1), u = p / n_ff, r = p % n_ff;
-            return base + (uint64_t)uid[u] * stride + ((i & 1) ? ou : og) + (uint64_t)r * rb;
+    uint8_t *ring = smem + al16((size_t)((uint8_t *)(xd + NT * (a.K / 32)) - smem));
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nt = a.src.n_tok, K = a.K, n_ff = a.n_ff, rb = a.rb_gu;
+    const uint32_t ch = a.chunk, S = a.slots;
+    const uint32_t slot_bytes = 2u * ch * rb;
+    const KArgs ka = kargs();
+    const bool uniq = a.src.unique != 0;
+    // the host list's ids, loaded while the block starts up (lane u: id u)
+    const int32_t hid = (uniq && wave < kProd) ? host_ids(ka, a.src.n_fixed) : -1;
+    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
+    if (!uniq && tid < 64) build_plan(P, a.src, tid);
+    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
+    const uint32_t PT = nu * n_ff;
+    const uint32_t p0 = (uint32_t)(((uint64_t)PT * blockIdx.x) / gridDim.x);
+    const uint32_t p1 = (uint32_t)(((uint64_t)PT * (blockIdx.x + 1)) / gridDim.x);
+    const uint32_t np = p1 - p0;
+    const uint32_t C = (np + ch - 1) / ch;
+
+    if (wave < kProd) {
+        const uint8_t *base = a.base;
+        const uint64_t stride = a.stride, og = a.og, ou = a.ou;
+        // every expert id in one register (lane u holds id u): a segment's id
+        // is then one v_readlane, not a memory round trip
+        const int32_t idv = uniq ? hid : (lane < nu ? P->uid[lane] : -1);
+        uint32_t issued = 0;
+        Q4MI_TR(0, 0, tid == 0);
+        auto issue = [&](uint32_t c) {
+            const uint32_t q0 = p0 + c * ch, q1 = min(q0 + ch, p1);
+            uint8_t *sg = ring + (size_t)(c % S) * slot_bytes, *su = sg + (size_t)ch * rb;
+            for (uint32_t q = q0; q < q1;) {   // one expert's run of rows at a time
+                const uint32_t u = q / n_ff, r = q % n_ff;
+                const uint32_t n = min(q1 - q, n_ff - r);
+                const int32_t id = __builtin_amdgcn_readlane(idv, u);
+                const uint8_t *e = base + (uint64_t)id * stride + (uint64_t)r * rb;
+                issued += dma1<UNIT>(sg + (size_t)(q - q0) * rb, e + og, n * rb, lane);
+                issued += dma1<UNIT>(su + (size_t)(q - q0) * rb, e + ou, n * rb, lane);
+                q += n;
+            }
         };
-    };
-    // Weights and the decode table are fetched asynchronously into LDS
-    // first; x is loaded after them.  VMEM results return in issue order, so
-    // quantizing x waits for the whole fetch -- which compute needs anyway --
-    // and adds only the quantization itself to the critical path.
-    uint32_t pc = p0;
-    uint32_t n = min(a.chunk, p1 - pc);
-    if (n && !(a.dbg & 4)) stage_rows<UNIT>(tile0, src_of(pc), 2 * n, rb, wave, lane);
-    if (TY == Q4MI_T_IQ3_S && !(a.dbg & 1))
-        dma_copy((uint8_t *)stab, (const uint8_t *)a.stab, 32768, wave, lane);
-    if (!(a.dbg & 2)) {
-        const uint32_t quads = nt * (a.K / 4);
-        for (uint32_t i = tid; i < quads; i += kThreads) {
-            const float4 v = *(const float4 *)(a.x + (size_t)i * 4);
-            float dd;
-            int bs;
-            const uint32_t q = q4mi_quant_team8(v, &dd, &bs);
-            *(uint32_t *)(xq + (size_t)i * 4) = q;
-            if ((i & 7u) == 0) xd[i / 8] = dd;
-        }
+        auto items = [&](uint32_t c) { return min(ch, np - c * ch); };
+        produce(Y, P->ends[wave], wave, C, S, issued, issue, items,
+                [&](uint32_t c) { if (c < 12) Q4MI_TR(16 + c, 0, lane == 0); });
+        Q4MI_TR(2, 0, tid == 0);
+        return;
     }
-    wait_stage();
-    __syncthreads();
-    const uint32_t gi = tid % TPR, slot = tid / TPR;
-    constexpr uint32_t kSlots = kThreads / TPR;
+
+    // ---- consumers
+    const uint32_t ct = tid - kProd * 64;
+    const uint32_t cw = wave - kProd;               // consumer wave
+    // every prologue load is issued before any is used
+    const uint32_t nq = nt * K / 4;
+    const float4 *xg = (const float4 *)a.x;
+    const uint32_t code = (kIq && ct < 512) ? q4mi_iq3s_code_dev[ct] : 0u;
+    const float4 v0 = ct < nq ? xg[ct] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (kIq) build_stab(stab, code, ct);
+    if (ct < nq) quant_quad(v0, ct, xq, xd);
+    for (uint32_t i = ct + kCons; i < nq; i += kCons) quant_quad(xg[i], i, xq, xd);
+    if (lane == 0) atomicAdd(&Y->ready, 1u);
+    spin_ge(&Y->ready, kConsW);                     // table and q8(x) complete
+    Q4MI_TR(4, 0, ct == 0);
+    constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
+    const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
     XRegs<NT, GPT> xr;
-    load_xregs<NT, GPT, TPR>(xr, xq, xd, a.K, nt, gi);
-    uint32_t buf = 0;
-    while (n) {
-        wait_stage();
-        __syncthreads();                      // chunk landed in tile[buf]
-        uint8_t *tile = buf ? tile1 : tile0;
-        const uint32_t pn = pc + n;
-        const uint32_t nn = min(a.chunk, p1 - pn);
-        if (nn && !(a.dbg & 4)) stage_rows<UNIT>(buf ? tile0 : tile1, src_of(pn), 2 * nn, rb, wave, lane);
-        const uint32_t *tw = (const uint32_t *)tile;
-        for (uint32_t i = slot; i < n && !(a.dbg & 8); i += kSlots) {
-            const uint32_t p = pc + i, u = p / n_ff, r = p % n_ff;
-            const uint32_t sel = P->sel[u];
+    load_xregs<NT, GPT, TPR>(xr, xq, xd, K, nt, gi);
+    float *hout = a.h;
+    for (uint32_t b = cw * kTpw; b < np; b += kTeams) {   // b: this wave's first pair
+        const uint32_t bl = min(b + kTpw, np) - 1;
+        for (uint32_t c = b / ch; c <= bl / ch; c++) wait_chunk(Y, c);
+        if (b / kTeams < 4) Q4MI_TR(5 + 2 * (b / kTeams), 0, ct == 0);
+        const uint32_t i = b + sub;
+        if (i < np) {
+            const uint32_t c = i / ch, j = i % ch;
+            const uint8_t *tile = ring + (size_t)(c % S) * slot_bytes;
+            const uint32_t *tw = (const uint32_t *)tile;
+            const uint32_t p = p0 + i, u = p / n_ff, r = p % n_ff;
+            const uint32_t sel = uniq ? 1u : P->sel[u];
             float ag[NT], au[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.f;
@@ -360,7 +615,7 @@ __global__ __launch_bounds__(kThreads) void moe_gu_k(MoeArgs a, HostList hl) {
                     int32_t w[8];
                     int mult;
                     float d;
-                    group_w<TY>(stab, tile, tw, (2 * i + which) * rb, g, w, mult, d);
+                    group_w<TY>(stab, tile, tw, (which * ch + j) * rb, g, w, mult, d);
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         if (!((sel >> t) & 1u)) continue;
@@ -377,113 +632,123 @@ __global__ __launch_bounds__(kThreads) void moe_gu_k(MoeArgs a, HostList hl) {
             for (int t = 0; t < NT; t++) {
                 if (!((sel >> t) & 1u)) continue;
                 const float gs = rsum<TPR>(ag[t]), us = rsum<TPR>(au[t]);
-                if (gi == TPR - 1) hbuf[(p & 31u) * NT + t] = silu_f(gs) * us;
+                if (gi == TPR - 1) hout[((size_t)u * kMaxT + t) * n_ff + r] = silu_f(gs) * us;
             }
+            if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);   // rows of pair i read
         }
-        __syncthreads();                      // tile[buf] free; hbuf complete
-        if ((pn & 31u) == 0) {
-            // a 32-row unit is complete: q8 of h for every selected token
-            const uint32_t pu = pn - 32, u = pu / n_ff, r = pu % n_ff;
-            const uint32_t sel = P->sel[u];
-            if (tid < 8u * nt) {
-                const uint32_t t = tid >> 3, sub = tid & 7u;
-                if ((sel >> t) & 1u) {
-                    const float4 v = make_float4(hbuf[(4 * sub) * NT + t], hbuf[(4 * sub + 1) * NT + t],
-                                                 hbuf[(4 * sub + 2) * NT + t], hbuf[(4 * sub + 3) * NT + t]);
-                    float dd;
-                    int bs;
-                    const uint32_t q = q4mi_quant_team8(v, &dd, &bs);
-                    *(uint32_t *)(a.hq + ((size_t)u * kMaxT + t) * n_ff + r + 4 * sub) = q;
-                    if (sub == 0) a.hd[((size_t)u * kMaxT + t) * (n_ff / 32) + r / 32] = dd;
-                }
-            }
-        }
-        pc = pn;
-        n = nn;
-        buf ^= 1u;
+        if (b / kTeams < 4) Q4MI_TR(6 + 2 * (b / kTeams), 0, ct == 0);
     }
+    Q4MI_TR(30, 0, ct == 0);
 }
 
 // ---------------------------------------------------------------- down
+// Same roles.  Items are (expert u, output row rr); the chunks are runs of
+// `ch` experts (kDnRows rows each).  The consumers quantize every selected
+// h row (q8, 32-value groups) into LDS before computing.
+//
+// LDS: [stab] Plan Sync | part [kMaxU][NT][kDnRows] | hq [nsel_cap][n_ff] |
+//      hd [nsel_cap][n_ff/32] | ring of S slots, slot = ch experts x kDnRows
+//      rows.
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__global__ __launch_bounds__(kThreads) void moe_dn_k(MoeArgs a, HostList hl) {
+__global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    Q4MI_TR_DECL;
+    Q4MI_TR(31, 1, threadIdx.x == 0);
+    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
     uint32_t *stab = (uint32_t *)smem;
-    Plan *P = (Plan *)(smem + (TY == Q4MI_T_IQ3_S ? 32768 : 0));
-    float *part = (float *)(P + 1);                           // [kMaxU][kMaxT][kDnRows]
-    int8_t *hq = (int8_t *)(part + kMaxU * kMaxT * kDnRows);  // [nsel][n_ff]
-    float *hd = (float *)(hq + kMaxU * a.n_ff);               // [nsel][n_ff/32]
-    uint8_t *tile0 = (uint8_t *)(hd + kMaxU * (a.n_ff / 32));
-    uint8_t *tile1 = tile0 + (size_t)a.chunk * kDnRows * a.rb_dn;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-    if (tid < 64) build_plan(P, a.src, hl, tid);
-    __syncthreads();
-    const uint32_t nu = P->nu;
-    const uint32_t nt = a.src.n_tok;
+    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
+    Sync *Y = (Sync *)(P + 1);
+    float *part = (float *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));   // [kMaxU][NT][kDnRows]
+    int8_t *hq = (int8_t *)(part + kMaxU * NT * kDnRows);
+    const uint32_t n_ff = a.n_ff, cap = a.nsel_cap;
+    float *hd = (float *)(hq + (size_t)cap * n_ff);
+    uint8_t *ring = smem + al16((size_t)((uint8_t *)(hd + (size_t)cap * (n_ff / 32)) - smem));
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nt = a.src.n_tok, rb = a.rb_dn;
+    const uint32_t ch = a.chunk, S = a.slots;
     const uint32_t r0 = blockIdx.x * kDnRows;
     const uint32_t nr = min(kDnRows, a.n_embd - r0);
-    const uint32_t rb = a.rb_dn;
-    const uint8_t *base = a.base;
-    const uint64_t stride = a.stride, od = a.od;
-    const int32_t *uid = P->uid;
-    auto src_of = [=](uint32_t u0) {
-        return [=](uint32_t i) -> const uint8_t * {
-            const uint32_t u = u0 + i / nr, r = r0 + i % nr;
-            return base + (uint64_t)uid[u] * stride + od + (uint64_t)r * rb;
+    const uint32_t slot_bytes = ch * kDnRows * rb;
+    const KArgs ka = kargs();
+    const bool uniq = a.src.unique != 0;
+    // the host list's ids (producers) or weights (consumers), loaded while
+    // the block starts up (lane u: entry u)
+    const int32_t hword = !uniq ? 0 : wave < kProd ? host_ids(ka, a.src.n_fixed)
+                                                  : __builtin_bit_cast(int32_t, host_weights(ka, a.src.n_fixed));
+    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
+    if (!uniq && tid < 64) build_plan(P, a.src, tid);
+    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
+    const uint32_t nsel = uniq ? nu : P->nsel;
+    const uint32_t C = (nu + ch - 1) / ch;
+    const float *hg = a.h;
+
+    if (wave < kProd) {
+        const uint8_t *base = a.base;
+        const uint64_t stride = a.stride, od = a.od;
+        const int32_t idv = uniq ? hword : (lane < nu ? P->uid[lane] : -1);
+        uint32_t issued = 0;
+        Q4MI_TR(0, 1, tid == 0);
+        auto issue = [&](uint32_t c) {
+            const uint32_t e0 = c * ch, e1 = min(e0 + ch, nu);
+            uint8_t *dst = ring + (size_t)(c % S) * slot_bytes;
+            for (uint32_t u = e0; u < e1; u++) {
+                const int32_t id = __builtin_amdgcn_readlane(idv, u);
+                const uint8_t *e = base + (uint64_t)id * stride + od + (uint64_t)r0 * rb;
+                issued += dma1<UNIT>(dst + (size_t)(u - e0) * nr * rb, e, nr * rb, lane);
+            }
         };
-    };
-    // y of this block's rows, needed at the very end: load it first
-    float yv = 0.f;
-    if (tid < nt * nr) yv = a.y[(size_t)(tid / nr) * a.n_embd + r0 + tid % nr];
-    // weights, table and the q8 of h, all asynchronously into LDS
-    uint32_t uc = 0;
-    uint32_t n = min(a.chunk, nu);
-    if (n && !(a.dbg & 64)) stage_rows<UNIT>(tile0, src_of(0), n * nr, rb, wave, lane);
-    if (TY == Q4MI_T_IQ3_S && !(a.dbg & 16))
-        dma_copy((uint8_t *)stab, (const uint8_t *)a.stab, 32768, wave, lane);
-    if (!(a.dbg & 32)) {
-        const uint32_t n_ff = a.n_ff;
-        const Plan *PP = P;
-        const int8_t *ghq = a.hq;
-        const float *ghd = a.hd;
-        // pair slot -> (u, t): the slots of u are its selected tokens in order
-        auto pair_ut = [=](uint32_t slot, uint32_t &u, uint32_t &t) {
-            u = 0;
-            while (u + 1 < nu && PP->pslot[u + 1] <= slot) u++;
-            uint32_t sel = PP->sel[u], kk = slot - PP->pslot[u];
-            t = 0;
-            for (;; t++)
-                if ((sel >> t) & 1u) {
-                    if (!kk) break;
-                    kk--;
-                }
-        };
-        stage_rows<16>((uint8_t *)hq, [=](uint32_t i) -> const uint8_t * {
-            uint32_t u, t;
-            pair_ut(i, u, t);
-            return (const uint8_t *)(ghq + ((size_t)u * kMaxT + t) * n_ff);
-        }, P->nsel, n_ff, wave, lane);
-        stage_rows<4>((uint8_t *)hd, [=](uint32_t i) -> const uint8_t * {
-            uint32_t u, t;
-            pair_ut(i, u, t);
-            return (const uint8_t *)(ghd + ((size_t)u * kMaxT + t) * (n_ff / 32));
-        }, P->nsel, n_ff / 8, wave, lane);
+        auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
+        produce(Y, P->ends[wave], wave, C, S, issued, issue, items,
+                [&](uint32_t c) { if (c < 12) Q4MI_TR(16 + c, 1, lane == 0); });
+        Q4MI_TR(2, 1, tid == 0);
+        return;
     }
-    const uint32_t gi = tid % TPR, slot = tid / TPR;
-    constexpr uint32_t kSlots = kThreads / TPR;
-    uint32_t buf = 0;
-    while (n) {
-        wait_stage();
-        __syncthreads();
-        uint8_t *tile = buf ? tile1 : tile0;
-        const uint32_t un = uc + n;
-        const uint32_t nn = min(a.chunk, nu - un);
-        if (nn) stage_rows<UNIT>(buf ? tile0 : tile1, src_of(un), nn * nr, rb, wave, lane);
-        const uint32_t *tw = (const uint32_t *)tile;
-        for (uint32_t it = slot; it < n * nr && !(a.dbg & 128); it += kSlots) {
-            const uint32_t u = uc + it / nr, rr = it % nr;
-            const uint32_t sel = P->sel[u];
-            const uint32_t ps = P->pslot[u];
+
+    // ---- consumers
+    const uint32_t ct = tid - kProd * 64;
+    const uint32_t cw = wave - kProd;
+    // y of this block's rows and the host list's weights (needed at the end;
+    // loaded now, weight u in lane u)
+    float yv = 0.f;
+    if (ct < nt * nr) yv = a.y[(size_t)(ct / nr) * a.n_embd + r0 + ct % nr];
+    const float wv = __builtin_bit_cast(float, hword);
+    // q8 of every selected h row; pair slot s holds h[u][t] (slots of u are
+    // its selected tokens in order).  Every prologue load is issued before
+    // any is used.
+    const uint32_t qpr = n_ff / 4, nq = nsel * qpr;
+    auto hquad = [&](uint32_t i) -> const float4 * {
+        const uint32_t s = i / qpr;
+        const uint32_t row = uniq ? s * kMaxT : P->prow[s];
+        return (const float4 *)(hg + (size_t)row * n_ff) + i % qpr;
+    };
+    const uint32_t code = (kIq && ct < 512) ? q4mi_iq3s_code_dev[ct] : 0u;
+    const float4 v0 = ct < nq ? *hquad(ct) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v1 = ct + kCons < nq ? *hquad(ct + kCons) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (kIq) build_stab(stab, code, ct);
+    if (ct < nq) quant_quad(v0, ct, hq, hd);
+    if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
+    for (uint32_t i = ct + 2 * kCons; i < nq; i += kCons) quant_quad(*hquad(i), i, hq, hd);
+    if (lane == 0) atomicAdd(&Y->ready, 1u);
+    spin_ge(&Y->ready, kConsW);                     // table and q8(h) complete
+    Q4MI_TR(4, 1, ct == 0);
+    constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
+    const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
+    const uint32_t ni = nu * nr;                    // items, expert-major
+    const uint32_t ipc = ch * nr;                   // items per chunk
+    for (uint32_t b = cw * kTpw; b < ni; b += kTeams) {
+        const uint32_t bl = min(b + kTpw, ni) - 1;
+        for (uint32_t c = b / ipc; c <= bl / ipc; c++) wait_chunk(Y, c);
+        if (b / kTeams < 4) Q4MI_TR(5 + 2 * (b / kTeams), 1, ct == 0);
+        const uint32_t it = b + sub;
+        if (it < ni) {
+            const uint32_t c = it / ipc, jj = it % ipc;
+            const uint8_t *tile = ring + (size_t)(c % S) * slot_bytes;
+            const uint32_t *tw = (const uint32_t *)tile;
+            const uint32_t u = it / nr, rr = it % nr;
+            const uint32_t sel = uniq ? 1u : P->sel[u];
+            const uint32_t ps = uniq ? u : P->pslot[u];
             float acc[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) acc[t] = 0.f;
@@ -493,13 +758,13 @@ __global__ __launch_bounds__(kThreads) void moe_dn_k(MoeArgs a, HostList hl) {
                 int32_t w[8];
                 int mult;
                 float d;
-                group_w<TY>(stab, tile, tw, it * rb, g, w, mult, d);
+                group_w<TY>(stab, tile, tw, jj * rb, g, w, mult, d);
                 uint32_t s2 = ps;
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     if (!((sel >> t) & 1u)) continue;
-                    const int4 qa = *(const int4 *)(hq + (size_t)s2 * a.n_ff + 32 * g);
-                    const int4 qb = *(const int4 *)(hq + (size_t)s2 * a.n_ff + 32 * g + 16);
+                    const int4 qa = *(const int4 *)(hq + (size_t)s2 * n_ff + 32 * g);
+                    const int4 qb = *(const int4 *)(hq + (size_t)s2 * n_ff + 32 * g + 16);
                     int s = 0;
                     s = q4mi_sdot4(w[0], qa.x, s);
                     s = q4mi_sdot4(w[1], qa.y, s);
@@ -509,107 +774,150 @@ __global__ __launch_bounds__(kThreads) void moe_dn_k(MoeArgs a, HostList hl) {
                     s = q4mi_sdot4(w[5], qb.y, s);
                     s = q4mi_sdot4(w[6], qb.z, s);
                     s = q4mi_sdot4(w[7], qb.w, s);
-                    acc[t] = fmaf((float)(s * mult), d * hd[(size_t)s2 * (a.n_ff / 32) + g], acc[t]);
+                    acc[t] = fmaf((float)(s * mult), d * hd[(size_t)s2 * (n_ff / 32) + g], acc[t]);
                     s2++;
                 }
             }
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const float v = ((sel >> t) & 1u) ? rsum<TPR>(acc[t]) : 0.f;
-                if (gi == TPR - 1) part[((size_t)u * kMaxT + t) * kDnRows + rr] = v;
+                if (gi == TPR - 1) part[((size_t)u * NT + t) * kDnRows + rr] = v;
             }
+            if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);
         }
-        __syncthreads();
-        uc = un;
-        n = nn;
-        buf ^= 1u;
+        if (b / kTeams < 4) Q4MI_TR(6 + 2 * (b / kTeams), 1, ct == 0);
     }
-    __syncthreads();
-    // y[t][r] += sum_u w[u][t] * pd[u][t][r], u in plan order
-    for (uint32_t i = tid; i < nt * nr; i += kThreads) {   // nt * nr <= kThreads
-        const uint32_t t = i / nr, rr = i % nr;
+    if (lane == 0) atomicAdd(&Y->fin, 1u);
+    spin_ge(&Y->fin, kConsW);                       // every partial sum written
+    Q4MI_TR(29, 1, ct == 0);
+    // y[t][r] += sum_u w[u][t] * part[u][t][r], u in plan order
+    if (ct < nt * nr) {
+        const uint32_t t = ct / nr, rr = ct % nr;
         float s = 0.f;
-        for (uint32_t u = 0; u < nu; u++)
-            if ((P->sel[u] >> t) & 1u) s += P->w[u][t] * part[((size_t)u * kMaxT + t) * kDnRows + rr];
+        if (uniq) {
+            for (uint32_t u = 0; u < nu; u++)
+                s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), u)) *
+                     part[(size_t)u * NT * kDnRows + rr];
+        } else {
+            for (uint32_t u = 0; u < nu; u++)
+                if ((P->sel[u] >> t) & 1u) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
+        }
         a.y[(size_t)t * a.n_embd + r0 + rr] = yv + s;
     }
+    Q4MI_TR(30, 1, ct == 0);
+}
+
+// ------------------------------------------------------------------ host
+constexpr size_t kLdsCap = 160 * 1024;
+
+static size_t head_bytes(uint32_t ty) {
+    return al16((ty == Q4MI_T_IQ3_S ? 32768 : 0) + sizeof(Plan) + sizeof(Sync));
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>
-static bool launch_gu(MoeArgs a, const HostList &hl, uint32_t nu_host) {
-    const size_t fixed = (TY == Q4MI_T_IQ3_S ? 32768 : 0) + sizeof(Plan) + (size_t)NT * a.K +
-                         (size_t)NT * (a.K / 32) * 4 + 32 * NT * 4;
-    // pairs per chunk (two rows each; a divisor of the 32-row unit), two
-    // chunk buffers in LDS
-    uint32_t ch = 16;
-    const size_t lds_cap = 150 * 1024;
-    while (ch > 1 && fixed + 4ull * ch * a.rb_gu + 64 > lds_cap) ch /= 2;
-    a.chunk = ch;
-    const size_t lds = fixed + 4ull * ch * a.rb_gu + 64;
-    const bool wide = ((((uintptr_t)a.base) | a.stride | a.og | a.ou | a.rb_gu) & 15u) == 0;
-    const void *fn = wide ? (const void *)moe_gu_k<TY, NT, TPR, GPT, 16>
-                          : (const void *)moe_gu_k<TY, NT, TPR, GPT, 4>;
-    if (!ch || lds > lds_cap ||
-        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess) {
+static bool launch_gu(MoeArgs a, uint32_t nu_host) {
+    const uint32_t grid = (uint32_t)cu_count();
+    // one chunk per producer wave when it fits (a producer publishes a chunk
+    // only after issuing everything before it, so a second chunk would
+    // delay the first); device lists (unknown share) use 8 pairs
+    const uint32_t pairs = nu_host ? nu_host * a.n_ff : kMaxU * a.n_ff;
+    const uint32_t share = (pairs + grid - 1) / grid;
+    uint32_t ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : 8;
+    const size_t fixed = head_bytes(TY) + al16((size_t)NT * a.K + (size_t)NT * (a.K / 32) * 4);
+    uint32_t S = 0;
+    // A consumer wave waits for every chunk its two pairs touch (at most
+    // two), so a reused ring needs three slots to always make progress.
+    for (;; ch = (ch + 1) / 2) {
+        const size_t slot = 2ull * ch * a.rb_gu;
+        S = fixed < kLdsCap ? (uint32_t)std::min<size_t>(kMaxS, (kLdsCap - fixed) / slot) : 0;
+        if (S >= 3 || ch == 1) break;
+    }
+    const uint32_t C = (share + ch - 1) / ch;
+    if (S < 3 && S < C) {
         set_error("moe_gu_k: LDS limit");
         return false;
     }
-    // one block per CU, fewer when there is little work
-    const uint32_t pairs = (nu_host ? nu_host : kMaxU) * a.n_ff;
-    uint32_t grid = (uint32_t)cu_count();
-    if (grid > pairs / 4) grid = pairs / 4 > 0 ? pairs / 4 : 1;
+    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
+    a.chunk = ch;
+    a.slots = S;
+    const size_t lds = fixed + (size_t)S * 2 * ch * a.rb_gu;
+    const bool wide = ((((uintptr_t)a.base) | a.stride | a.og | a.ou | a.rb_gu) & 15u) == 0;
+    const void *fn = wide ? (const void *)moe_gu_k<TY, NT, TPR, GPT, 16>
+                          : (const void *)moe_gu_k<TY, NT, TPR, GPT, 4>;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        set_error("moe_gu_k: LDS limit (%zu)", lds);
+        return false;
+    }
     if (wide)
-        moe_gu_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kThreads), lds, stream()>>>(a, hl);
+        moe_gu_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
     else
-        moe_gu_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kThreads), lds, stream()>>>(a, hl);
+        moe_gu_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
     return launch_ok("moe_gu_k");
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>
-static bool launch_dn(MoeArgs a, const HostList &hl) {
-    const size_t fixed = (TY == Q4MI_T_IQ3_S ? 32768 : 0) + sizeof(Plan) +
-                         (size_t)kMaxU * kMaxT * kDnRows * 4 + (size_t)kMaxU * a.n_ff +
-                         (size_t)kMaxU * (a.n_ff / 32) * 4;
-    static_assert(kMaxT * kDnRows <= kThreads, "final reduce assumes one pass");
-    uint32_t ch = 16;   // experts per chunk, two chunk buffers in LDS
-    const size_t lds_cap = 150 * 1024;
-    while (ch > 1 && fixed + 2ull * ch * kDnRows * a.rb_dn + 64 > lds_cap) ch--;
+static bool launch_dn(MoeArgs a, uint32_t nu_host) {
+    const uint32_t cap = nu_host ? nu_host : kMaxU;   // selected pairs (<= 64)
+    const size_t fixed = head_bytes(TY) + (size_t)kMaxU * NT * kDnRows * 4 +
+                         al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
+    const uint32_t nu_est = nu_host ? nu_host : kMaxU;
+    uint32_t ch = std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd);
+    uint32_t S = 0;
+    for (;; ch = (ch + 1) / 2) {
+        const size_t slot = (size_t)ch * kDnRows * a.rb_dn;
+        S = fixed < kLdsCap ? (uint32_t)std::min<size_t>(kMaxS, (kLdsCap - fixed) / slot) : 0;
+        if (S >= 2 || ch == 1) break;
+    }
+    // a consumer wave's four items touch at most two chunks (ch * kDnRows >= 8)
+    const uint32_t C = (nu_est + ch - 1) / ch;
+    if (S < 2 && S < C) {
+        set_error("moe_dn_k: LDS limit");
+        return false;
+    }
+    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
     a.chunk = ch;
-    const size_t lds = fixed + 2ull * ch * kDnRows * a.rb_dn + 64;
-    const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | a.rb_dn) & 15u) == 0 &&
-                      a.n_embd % kDnRows == 0;
+    a.slots = S;
+    a.nsel_cap = cap;
+    const size_t lds = fixed + (size_t)S * ch * kDnRows * a.rb_dn;
+    const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | a.rb_dn) & 15u) == 0;
     const void *fn = wide ? (const void *)moe_dn_k<TY, NT, TPR, GPT, 16>
                           : (const void *)moe_dn_k<TY, NT, TPR, GPT, 4>;
-    if (!ch || lds > lds_cap ||
-        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess) {
-        set_error("moe_dn_k: LDS limit");
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        set_error("moe_dn_k: LDS limit (%zu)", lds);
         return false;
     }
     const uint32_t grid = (a.n_embd + kDnRows - 1) / kDnRows;
     if (wide)
-        moe_dn_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kThreads), lds, stream()>>>(a, hl);
+        moe_dn_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
     else
-        moe_dn_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kThreads), lds, stream()>>>(a, hl);
+        moe_dn_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
     return launch_ok("moe_dn_k");
 }
 
+// Gate/up lanes per pair: 32 (two or more groups per lane, two pairs per
+// wave) while the activation registers stay small, else the row layout.
+static RowLayout gu_layout(uint32_t G, int NT) {
+    if (G >= 64 && G % 32 == 0 && (G / 32) * (uint32_t)NT <= 4) return RowLayout{32, (int)(G / 32)};
+    return layout_for(G);
+}
+
 template <uint32_t TY, int NT>
-static bool gu_dispatch(const MoeArgs &a, const HostList &hl, uint32_t nu_host) {
-    const RowLayout L = layout_for(a.K / 32);
+static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
+    const RowLayout L = gu_layout(a.K / 32, NT);
 #define Q4MI_L(T, P) \
-    if (L.tpr == T && L.gpt == P) return launch_gu<TY, NT, T, P>(a, hl, nu_host);
+    if (L.tpr == T && L.gpt == P) return launch_gu<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+    if constexpr (NT <= 2) { Q4MI_L(32, 2) }
+    if constexpr (NT == 1) { Q4MI_L(32, 4) }
 #undef Q4MI_L
     return false;
 }
 
 template <uint32_t TY, int NT>
-static bool dn_dispatch(const MoeArgs &a, const HostList &hl) {
+static bool dn_dispatch(const MoeArgs &a, uint32_t nu_host) {
     const RowLayout L = layout_for(a.n_ff / 32);
 #define Q4MI_L(T, P) \
-    if (L.tpr == T && L.gpt == P) return launch_dn<TY, NT, T, P>(a, hl);
+    if (L.tpr == T && L.gpt == P) return launch_dn<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
 #undef Q4MI_L
     return false;
@@ -619,17 +927,25 @@ static bool dn_dispatch(const MoeArgs &a, const HostList &hl) {
 // (default both).  Lets a benchmark time each kernel of the pair alone.
 static int g_phases = 3;
 
+#ifdef Q4MI_TRACE
+static unsigned long long *g_trace = nullptr;
+extern "C" int q4mi_trace_read(void *dst, int kern) {
+    if (!g_trace || hipDeviceSynchronize() != hipSuccess) return 0;
+    return hipMemcpy(dst, g_trace + (size_t)kern * 4096 * 32, 4096 * 32 * 8,
+                     hipMemcpyDeviceToHost) == hipSuccess;
+}
+#endif
+
 template <int NT>
-static bool run_nt(uint32_t ty_gu, uint32_t ty_dn, const MoeArgs &a, const HostList &hl,
-                   uint32_t nu_host) {
+static bool run_nt(uint32_t ty_gu, uint32_t ty_dn, const MoeArgs &a, uint32_t nu_host) {
     if (g_phases & 1) {
-        const bool ok = ty_gu == Q4MI_T_IQ3_S ? gu_dispatch<Q4MI_T_IQ3_S, NT>(a, hl, nu_host)
-                                              : gu_dispatch<Q4MI_T_Q8_0, NT>(a, hl, nu_host);
+        const bool ok = ty_gu == Q4MI_T_IQ3_S ? gu_dispatch<Q4MI_T_IQ3_S, NT>(a, nu_host)
+                                              : gu_dispatch<Q4MI_T_Q8_0, NT>(a, nu_host);
         if (!ok) return false;
     }
     if (!(g_phases & 2)) return true;
-    return ty_dn == Q4MI_T_IQ3_S ? dn_dispatch<Q4MI_T_IQ3_S, NT>(a, hl)
-                                 : dn_dispatch<Q4MI_T_Q8_0, NT>(a, hl);
+    return ty_dn == Q4MI_T_IQ3_S ? dn_dispatch<Q4MI_T_IQ3_S, NT>(a, nu_host)
+                                 : dn_dispatch<Q4MI_T_Q8_0, NT>(a, nu_host);
 }
 
 // Rows are staged with 4- or 16-byte copies, so a row's byte size must be a
@@ -648,10 +964,8 @@ static bool shape_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uin
 }
 
 bool moe_warm(uint32_t n_ff) {
-    // q8 of h: kMaxU * kMaxT * n_ff codes + their fp32 scales
-    if (!ensure_pd((size_t)kMaxU * kMaxT * n_ff / 4 + (size_t)kMaxU * kMaxT * n_ff / 32 + 64))
-        return false;
-    return iq3s_signed_table() != nullptr;
+    // fp32 h of every (unique expert, token) pair
+    return ensure_pd((size_t)kMaxU * kMaxT * n_ff);
 }
 
 // Common driver.  All checks happen before the first launch so that a false
@@ -673,12 +987,16 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
         set_error("moe: x must be 16-byte aligned");
         return false;
     }
+    if (((uintptr_t)d_y & 3)) {
+        set_error("moe: y must be 4-byte aligned");
+        return false;
+    }
     if ((((uintptr_t)base) | stride | og | ou | od) & 3u) {
         set_error("moe: expert arena offsets must be 4-byte aligned");
         return false;
     }
     if (!moe_warm(n_ff)) return false;
-    MoeArgs a;
+    MoeArgs a = {};
     a.base = base;
     a.stride = stride;
     a.og = og;
@@ -689,26 +1007,21 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     a.n_embd = n_embd;
     a.rb_gu = (uint32_t)q4mi_row_bytes(gt, in_dim);
     a.rb_dn = (uint32_t)q4mi_row_bytes(dt, n_ff);
-    a.chunk = 0;
     a.x = d_x;
-    a.hq = (int8_t *)scratch().pd;
-    a.hd = (float *)((int8_t *)scratch().pd + (size_t)kMaxU * kMaxT * n_ff);
+    a.h = scratch().pd;
     a.y = d_y;
-    a.stab = iq3s_signed_table();
     a.src = src;
-    {
-        static int dbg = -1;
-        if (dbg < 0) {
-            const char *e = getenv("Q4MI_DBG");
-            dbg = e ? atoi(e) : 0;
-        }
-        a.dbg = (uint32_t)dbg;
-    }
+    a.hl = hl;
+#ifdef Q4MI_TRACE
+    if (!g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
+        (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
+    a.trace = g_trace;
+#endif
     const uint32_t nt = src.n_tok;
-    if (nt == 1) return run_nt<1>(gt, dt, a, hl, nu_host);
-    if (nt == 2) return run_nt<2>(gt, dt, a, hl, nu_host);
-    if (nt <= 4) return run_nt<4>(gt, dt, a, hl, nu_host);
-    return run_nt<8>(gt, dt, a, hl, nu_host);
+    if (nt == 1) return run_nt<1>(gt, dt, a, nu_host);
+    if (nt == 2) return run_nt<2>(gt, dt, a, nu_host);
+    if (nt <= 4) return run_nt<4>(gt, dt, a, nu_host);
+    return run_nt<8>(gt, dt, a, nu_host);
 }
 
 }  // namespace q4mi
@@ -722,12 +1035,11 @@ extern "C" {
 /* Benchmark hook: 1 = gate/up launch only, 2 = down only, 3 = both. */
 void q4mi_moe_phases(int mask) { g_phases = mask & 3; }
 
-/* Allocate the decode scratch and tables (call before any stream capture). */
+/* Allocate the decode scratch (call before any stream capture). */
 void q4_hip_moe_scratch_warm(void) {
     (void)moe_warm(1024);
     q4_mmvq_warm();
 }
-
 /* One token, n (<=64) experts given as HOST arrays: slot ids (expert index
  * into the arena) and routing weights.  d_y += sum_e wts[e] * FFN_e(x).
  * d_h, d_h2, d_down are accepted for ABI compatibility with the reference

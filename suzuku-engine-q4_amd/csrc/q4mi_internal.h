@@ -28,9 +28,6 @@ bool ensure_xq(size_t elems);
 
 // Compute units of the current device (persistent grids size to it).
 int cu_count();
-// 8192-entry signed IQ3_S table in device memory (built on first use;
-// call before any graph capture).
-const uint32_t *iq3s_signed_table();
 
 // Error reporting: entry points return false; the last message is kept.
 void set_error(const char *fmt, ...);

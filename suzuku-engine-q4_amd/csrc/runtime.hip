@@ -94,34 +94,4 @@ int cu_count() {
     return n;
 }
 
-// Signed IQ3_S table: entry (s4 << 9 | idx) = the 4 grid magnitudes of idx
-// as int8 with the bytes whose sign bit is set in s4 negated.
-__global__ void iq3s_signed_k(uint32_t *t) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= 8192) return;
-    const uint32_t c = q4mi_iq3s_code_dev[i & 511u];
-    uint32_t g = 0;
-    for (int j = 0; j < 4; j++) g |= (2u * ((c >> (3 * j)) & 7u) + 1u) << (8 * j);
-    t[i] = (uint32_t)q4mi_sign4(g, q4mi_expand4(i >> 9));
-}
-
-static uint32_t *g_signed = nullptr;
-
-const uint32_t *iq3s_signed_table() {
-    if (g_signed) return g_signed;
-    uint32_t *t = nullptr;
-    if (hipMalloc(&t, 8192 * sizeof(uint32_t)) != hipSuccess) {
-        set_error("iq3s table: hipMalloc failed");
-        return nullptr;
-    }
-    iq3s_signed_k<<<32, 256, 0, stream()>>>(t);
-    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream()) != hipSuccess) {
-        set_error("iq3s table: build failed");
-        (void)hipFree(t);
-        return nullptr;
-    }
-    g_signed = t;
-    return g_signed;
-}
-
 }  // namespace q4mi

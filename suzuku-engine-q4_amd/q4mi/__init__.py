@@ -15,7 +15,8 @@ import ctypes
 import os
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG, "lib", "libq4mi.so")
+# Q4MI_LIB selects another build of the same library (same ABI).
+LIB_PATH = os.environ.get("Q4MI_LIB") or os.path.join(PKG, "lib", "libq4mi.so")
 
 T_Q8_0 = 8
 T_IQ3_S = 21
