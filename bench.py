@@ -35,6 +35,20 @@ LAYER_BYTES = 11 * EXPERT_BYTES + 2 * 4 * N_EMBD   # 14,884,864
 GU_BYTES = 11 * 901120 + 4 * N_EMBD
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy);
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "moe_decode_config2_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch " + kernel + ":"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def routes(rng, L):
     import numpy as np
     out = []
@@ -218,7 +232,8 @@ def main():
         "kernel_us": {"moe_gu_k": round(t_gu * 1e6, 3), "moe_dn_k": round(t_dn * 1e6, 3)},
         "single_layer_latency_us": round(single_us, 2),
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 2), "peak": HBM_PEAK,
-                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK, 4),
+                     "traffic": measured_traffic("moe_gu_k"),
                      "kernel": "moe_gu_k", "bytes_per_launch": GU_BYTES},
     }
     del g_full, g_gu, g_dn, arenas

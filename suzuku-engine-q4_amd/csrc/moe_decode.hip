@@ -879,7 +879,10 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
     a.slots = S;
     a.nsel_cap = cap;
     const size_t lds = fixed + (size_t)S * ch * kDnRows * a.rb_dn;
-    const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | a.rb_dn) & 15u) == 0;
+    // a block copies one contiguous run of kDnRows rows per expert: 16-byte
+    // units need that run (not each row) 16-byte aligned and sized
+    const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | ((uint64_t)kDnRows * a.rb_dn)) & 15u) == 0 &&
+                      a.n_embd % kDnRows == 0;
     const void *fn = wide ? (const void *)moe_dn_k<TY, NT, TPR, GPT, 16>
                           : (const void *)moe_dn_k<TY, NT, TPR, GPT, 4>;
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
