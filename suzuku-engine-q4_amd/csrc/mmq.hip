@@ -102,23 +102,29 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
 // 0,1 through LDS, which form h = silu(g)*u and write its q8 codes (the
 // 32 h columns of a q8 group are in the lane and its partner lane l^32).
 constexpr int MMQ_NB = 128;      // weight rows per block
+#ifndef MMQ_TP
+#define MMQ_TP 1                 // token sub-tiles whose MFMA chains overlap
+#endif
 constexpr int MMQ_MB = 128;      // token rows per block
-constexpr int MMQ_KH = 128;      // K values per activation stage
-constexpr int MMQ_ALD = MMQ_KH + 8;  // fp16 row stride of the activation tile
 
 template <uint32_t TY>
 struct RawSpec {
     static constexpr uint32_t SB = TY == Q4MI_T_IQ3_S ? 110u : 8u * 34u;  // bytes / 256 values
-    static constexpr uint32_t SS = (SB + 2u + 3u) / 4u * 4u;            // LDS slot bytes
+    // LDS slot: the dwords covering a superblock that starts 0 or 2 bytes into
+    // a dword, rounded to an even count (two staging threads per row)
+    static constexpr uint32_t SS = ((SB + 2u + 3u) / 4u + 1u) / 2u * 8u;
 };
 
+// Double-buffered stages of 64 K values (two q8 groups).  Activation rows
+// are 128 B (64 fp16 codes) with their eight 16-byte chunks XOR-swizzled by
+// the row index (chunk c of row r sits at c ^ (r & 7)), so one 1 KB copy
+// fills 8 whole rows and the MFMA operand reads of 32 rows hit distinct
+// banks.  Raw weight bytes are double-buffered per superblock.
 template <uint32_t TY>
 struct MmqLds {
-    _Float16 act[MMQ_MB][MMQ_ALD];          // 34.8 KB; reused for the fused hand-off
-    float dx[4][MMQ_MB];                    // group scales of the staged half
-    uint8_t raw[MMQ_NB][RawSpec<TY>::SS];   // raw weight bytes of this superblock
-    float dwb[MMQ_NB];                      // IQ3_S superblock scale per row
-    float dwg[8][MMQ_NB];                   // Q8_0 block scales per row
+    _Float16 act[2][MMQ_MB][64];            // 32 KB; reused for the fused hand-off
+    float dx[2][MMQ_MB][2];                 // group scales of each staged pair
+    uint8_t raw[2][MMQ_NB][RawSpec<TY>::SS];  // raw weight bytes per superblock
     uint2 g16[512];                         // IQ3_S grid as fp16 magnitudes
     uint2 sm16[16];                         // sign nibble -> fp16 sign masks
 };
@@ -200,24 +206,64 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
     }
 }
 
+// gfx950 global -> LDS copy of one wave (lane i's UNIT bytes land at LDS
+// address m0 + i*UNIT), as inline asm: the compiler does not track it, so
+// its conservative wait before every later LDS read (it would wait for all
+// copies in flight) is not emitted; this kernel waits with exact counts.
+template <uint32_t UNIT>
+__device__ inline void mmq_copy(const void *g, uint32_t lds_addr) {
+    lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
+    if constexpr (UNIT == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :: "v"(g), "s"(lds_addr) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                     :: "v"(g), "s"(lds_addr) : "memory", "m0");
+}
+__device__ inline uint32_t mmq_lds(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+#define MMQ_VM_CASE(n) case n: asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); break;
+// wait until at most n of this wave's copies are in flight (n <= 24 here)
+__device__ inline void mmq_wait(uint32_t n) {
+    switch (__builtin_amdgcn_readfirstlane(n)) {
+        MMQ_VM_CASE(0) MMQ_VM_CASE(1) MMQ_VM_CASE(2) MMQ_VM_CASE(3) MMQ_VM_CASE(4)
+        MMQ_VM_CASE(5) MMQ_VM_CASE(6) MMQ_VM_CASE(7) MMQ_VM_CASE(8) MMQ_VM_CASE(9)
+        MMQ_VM_CASE(10) MMQ_VM_CASE(11) MMQ_VM_CASE(12) MMQ_VM_CASE(13) MMQ_VM_CASE(14)
+        MMQ_VM_CASE(15) MMQ_VM_CASE(16) MMQ_VM_CASE(17) MMQ_VM_CASE(18) MMQ_VM_CASE(19)
+        MMQ_VM_CASE(20) MMQ_VM_CASE(21) MMQ_VM_CASE(22) MMQ_VM_CASE(23) MMQ_VM_CASE(24)
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+#undef MMQ_VM_CASE
+// workgroup barrier that leaves this kernel's copies in flight
+__device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <uint32_t TY, bool FUSED>
 __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
     constexpr uint32_t SB = RawSpec<TY>::SB;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6, kh = lane >> 5;
+    constexpr uint32_t SSD = RawSpec<TY>::SS / 4;             // raw slot dwords
+    constexpr uint32_t RAW_OPS = (MMQ_NB * SSD + 63) / 64;    // dword copies per superblock
+    constexpr uint32_t RAW_PER_WAVE = (RAW_OPS + 3) / 4;
+    constexpr uint32_t ST_OPS = 5;                            // copies per stage per wave
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int2 tinfo = a.tiles[ti];
     const uint32_t e = (uint32_t)tinfo.x;
     const int32_t rbase = a.bounds[e] + tinfo.y;
     const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), (uint32_t)MMQ_MB);
-    const uint32_t nts = (mrows + 31) / 32;    // token sub-tiles with rows
     const uint8_t *We = a.w + (uint64_t)e * a.estride;
     // weight row (within the expert) of tile row r
     const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
     auto wrow = [&](uint32_t r) -> uint32_t {
         return FUSED ? (r < 64 ? nblk + r : a.n_ff + nblk + (r - 64)) : nblk + r;
+    };
+    auto wsrc = [&](uint32_t r, uint32_t sbi) -> const uint8_t * {
+        return We + (uint64_t)wrow(r) * a.rb + (uint64_t)sbi * SB;
     };
 
     if (TY == Q4MI_T_IQ3_S) {
@@ -238,16 +284,66 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
             L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
         }
     }
-    // activation source row of this thread's staging slot (2 threads per row)
-    const uint32_t st_row = tid >> 1, st_half = tid & 1u;
-    int64_t xrow = -1;
-    if (st_row < mrows) {
-        const int32_t p = rbase + (int32_t)st_row;
-        xrow = a.act_row ? a.act_row[p] : p;
+    // source rows of this lane's copies: activation op m covers tile rows
+    // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
+    const _Float16 *arow_src[4];
+    bool arow_ok[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
+        arow_ok[m] = r < mrows;
+        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
+        const int64_t xr = a.act_row ? a.act_row[p] : p;
+        arow_src[m] = a.xq + (uint64_t)xr * a.K;
     }
-    // raw staging: 2 threads per weight row
-    const uint32_t rw_row = tid >> 1, rw_part = tid & 1u;
-    const uint8_t *wsrc_row = We + (uint64_t)wrow(rw_row) * a.rb;
+    const float *drow_src;
+    bool drow_ok;
+    {
+        const uint32_t r = 32 * wv + lane / 2;
+        drow_ok = r < mrows;
+        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
+        const int64_t xr = a.act_row ? a.act_row[p] : p;
+        drow_src = a.xd + (uint64_t)xr * (a.K / 32);
+    }
+    const uint32_t nsb = a.K / 256;
+    const uint32_t nst = 4 * nsb;                     // 64-value stages
+
+    // copies of stage s (activation codes + scales) into buffer s & 1
+    auto issue_stage = [&](uint32_t s) __attribute__((always_inline)) {
+        const uint32_t buf = s & 1u;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t j = wv + 4 * m;            // 8 rows per op
+            const uint32_t r = 8 * j + lane / 8;
+            const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
+            // rows past the tile's end copy a valid row's bytes (their
+            // outputs are never stored); one copy instruction either way
+            const _Float16 *src = arow_ok[m] ? arow_src[m] + s * 64 + c * 8 : arow_src[m];
+            mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
+        }
+        const float *dsrc = drow_ok ? drow_src + s * 2 + (lane & 1u) : drow_src;
+        mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
+    };
+    // copies of superblock sbi's raw weight bytes into buffer sbi & 1
+    auto issue_raw = [&](uint32_t sbi) __attribute__((always_inline)) {
+        const uint32_t buf = sbi & 1u;
+        uint8_t *base = &L.raw[buf][0][0];
+#pragma unroll
+        for (uint32_t m = 0; m < RAW_PER_WAVE; m++) {
+            const uint32_t j = wv + 4 * m;
+            uint32_t d = 64 * j + lane;                // slot dword, row-major
+            // opaque: recompute the source address per copy instead of
+            // keeping 14 hoisted row pointers live across the K loop
+            asm volatile("" : "+v"(d));
+            const uint32_t r = min(d / SSD, (uint32_t)MMQ_NB - 1u), dw = d % SSD;
+            const uint8_t *rs = wsrc(r, sbi);
+            const uint32_t nd = ((uint32_t)((uintptr_t)rs & 3u) + SB + 3u) / 4u;
+            const uint32_t *s32 = (const uint32_t *)((uintptr_t)rs & ~(uintptr_t)3);
+            // dwords past the slice re-read its first dword (stay in bounds)
+            const uint32_t *src = (j < RAW_OPS && dw < nd) ? s32 + dw : s32;
+            mmq_copy<4>(src, mmq_lds(base + 256u * j));
+        }
+    };
 
     f32x16_t acc[4], inner[4];
 #pragma unroll
@@ -256,89 +352,72 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
         inner[t] = f32x16_t{};
     }
     const uint32_t arow = 32 * wv + (lane & 31u);    // this lane's weight row in the tile
-    const uint32_t nsb = a.K / 256;
-    for (uint32_t sbi = 0; sbi < nsb; sbi++) {
-        __syncthreads();
-        {   // raw weight bytes of superblock sbi for row rw_row
-            const uint8_t *src = wsrc_row + (uint64_t)sbi * SB;
-            const uintptr_t a0 = (uintptr_t)src & ~(uintptr_t)3;
-            const uint32_t nd = (uint32_t)(((uintptr_t)src + SB + 3 - a0) / 4);
-            uint32_t *dst = (uint32_t *)&L.raw[rw_row][0];
-            const uint32_t *s32 = (const uint32_t *)a0;
-            for (uint32_t i = rw_part; i < nd; i += 2) dst[i] = s32[i];
-            if (rw_part == 0) {
-                if (TY == Q4MI_T_IQ3_S) {
-                    L.dwb[rw_row] = q4mi_h2f(*(const uint16_t *)src);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        L.dwg[j][rw_row] = q4mi_h2f(*(const uint16_t *)(src + 34 * j));
-                }
-            }
+    issue_raw(0);
+    issue_stage(0);
+    for (uint32_t s = 0; s < nst; s++) {
+        const uint32_t sbi = s >> 2, q = s & 3u;
+        // every wave is done with stage s-1 (and at a superblock start with
+        // superblock sbi-1): their buffers may be refilled
+        mmq_bar();
+        uint32_t later = 0;
+        if (q == 0 && sbi + 1 < nsb) {
+            issue_raw(sbi + 1);
+            later += RAW_PER_WAVE;
         }
-        for (uint32_t half = 0; half < 2; half++) {
-            if (half) __syncthreads();
-            {   // activation codes: K values [sbi*256 + half*128, +128) of 128 rows
-                uint4 *dst = (uint4 *)&L.act[st_row][st_half * 64];
-                if (xrow >= 0) {
-                    const uint4 *src = (const uint4 *)(a.xq + (uint64_t)xrow * a.K + sbi * 256 +
-                                                       half * 128 + st_half * 64);
+        if (s + 1 < nst) {
+            issue_stage(s + 1);
+            later += ST_OPS;
+        }
+        mmq_wait(later);                              // this wave's part of stage s is in
+        mmq_bar();                                    // everyone's part is
+        const uint32_t buf = s & 1u;
+        // the row's raw bytes start at the same offset inside its slot as
+        // in memory (the slot begins at the enclosing dword)
+        const uint32_t roff = (uint32_t)((uintptr_t)wsrc(arow, sbi) & 3u);
+        const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) dst[i] = src[i];
-                    if (st_half == 0) {
+        for (int gl = 0; gl < 2; gl++) {
+            const uint32_t j = 2 * q + gl;            // group inside the superblock
+            half8_t A0, A1;
+            decode_a<TY>(L, R, j, kh, A0, A1);
+            const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
 #pragma unroll
-                        for (int g = 0; g < 4; g++)
-                            L.dx[g][st_row] =
-                                a.xd[(uint64_t)xrow * (a.K / 32) + sbi * 8 + half * 4 + g];
-                    }
-                } else {
+            for (int tp = 0; tp < 4; tp += MMQ_TP) {  // MMQ_TP token sub-tiles at a time
+                f32x16_t sacc[MMQ_TP];
+                float dxv[MMQ_TP];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) dst[i] = make_uint4(0, 0, 0, 0);
-                    if (st_half == 0) {
-#pragma unroll
-                        for (int g = 0; g < 4; g++) L.dx[g][st_row] = 0.f;
-                    }
+                for (int u = 0; u < MMQ_TP; u++) {
+                    const uint32_t tok = 32 * (tp + u) + (lane & 31u);
+                    const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
+                    const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
+                    sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, f32x16_t{}, 0, 0, 0);
+                    sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, sacc[u], 0, 0, 0);
+                    dxv[u] = L.dx[buf][tok][gl];
                 }
-            }
-            __syncthreads();
-            // the row's raw bytes start at the same offset inside its slot as
-            // in memory (the slot begins at the enclosing dword)
-            const uint32_t roff =
-                (uint32_t)(((uintptr_t)(We + (uint64_t)wrow(arow) * a.rb + (uint64_t)sbi * SB)) & 3);
-            const uint8_t *R = &L.raw[arow][roff];
 #pragma unroll
-            for (int gg = 0; gg < 4; gg++) {
-                const uint32_t j = half * 4 + gg;    // group inside the superblock
-                half8_t A0, A1;
-                decode_a<TY>(L, R, j, kh, A0, A1);
+                for (int u = 0; u < MMQ_TP; u++) {
+                    const int t = tp + u;
+                    if (TY == Q4MI_T_IQ3_S) {
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    if ((uint32_t)t < nts) {
-                        const uint32_t tok = 32 * t + (lane & 31u);
-                        const half8_t B0 = *(const half8_t *)&L.act[tok][32 * gg + 8 * kh];
-                        const half8_t B1 = *(const half8_t *)&L.act[tok][32 * gg + 16 + 8 * kh];
-                        f32x16_t sacc = {};
-                        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, sacc, 0, 0, 0);
-                        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, sacc, 0, 0, 0);
-                        const float dxv = L.dx[gg][tok];
-                        if (TY == Q4MI_T_IQ3_S) {
+                        for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[u][i], dxv[u], inner[t][i]);
+                    } else {
 #pragma unroll
-                            for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 16; i++) {
-                                const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                                acc[t][i] = fmaf(sacc[i], dxv * L.dwg[j][n], acc[t][i]);
-                            }
+                        for (int i = 0; i < 16; i++) {
+                            const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
+                            const uint32_t no = (uint32_t)((uintptr_t)wsrc(n, sbi) & 3u);
+                            const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][no] + 34 * j));
+                            acc[t][i] = fmaf(sacc[u][i], dxv[u] * dw, acc[t][i]);
                         }
                     }
                 }
             }
         }
-        if (TY == Q4MI_T_IQ3_S) {
+        if (TY == Q4MI_T_IQ3_S && q == 3) {   // superblock done: acc += inner * d_w
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float dw = L.dwb[32 * wv + 8 * (i / 4) + 4 * kh + (i % 4)];
+                const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
+                const uint32_t no = (uint32_t)((uintptr_t)wsrc(n, sbi) & 3u);
+                const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][no]));
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     acc[t][i] = fmaf(inner[t][i], dw, acc[t][i]);
@@ -364,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     }
     // fused: waves 2,3 (up rows) hand their accumulators to waves 0,1
     __syncthreads();
-    float *ex = (float *)&L.act[0][0];   // [2 waves][4 t][16 i][64 lanes]
+    float *ex = (float *)&L.act[0][0][0];   // [2 waves][4 t][16 i][64 lanes] = 32 KB
     if (wv >= 2) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
