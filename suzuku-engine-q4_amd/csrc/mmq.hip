@@ -23,6 +23,8 @@
 // w + e*expert_stride_bytes, dst rows in xq order), q4_mmq_swiglu.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "q4mi_common.h"
 #include "q4mi_internal.h"
 
@@ -62,30 +64,47 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 }
 
 // --------------------------------------------------------------- tiles
-// tiles[i] = (expert, first row of its MT-row tile); *count = number of tiles.
+// One tile list, tiles[i] = (expert, first row), *count = its length.  Every
+// whole 128-row tile of an expert is listed; its remaining rows (if any)
+// form one more tile that the kernel runs with just enough 32-row
+// sub-tiles, so a tail of a few rows costs a 32-row tile, not a 128-row
+// one.  The list is ordered by tile size, largest first (longest work is
+// scheduled first).
 __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ bounds,
                                                    uint32_t n_exp, int2 *__restrict__ tiles,
-                                                   uint32_t *__restrict__ count,
-                                                   uint32_t max_tiles) {
+                                                   uint32_t *__restrict__ count, uint32_t cap) {
     __shared__ uint32_t s[512];
+    __shared__ uint32_t base;
     const uint32_t e = threadIdx.x;
-    uint32_t c = 0;
+    uint32_t n = 0;
     if (e < n_exp) {
-        const int32_t n = bounds[e + 1] - bounds[e];
-        c = n > 0 ? (uint32_t)((n + MT - 1) / MT) : 0u;
+        const int32_t v = bounds[e + 1] - bounds[e];
+        n = v > 0 ? (uint32_t)v : 0u;
     }
-    s[e] = c;
+    const uint32_t nfull = n / MT, tail = n % MT;
+    const uint32_t tcls = tail ? (tail + 31) / 32 - 1 : 4u;   // 4 = no tail tile
+    if (e == 0) base = 0;
+    for (int c = 3; c >= 0; c--) {
+        const uint32_t cnt = (c == 3 ? nfull : 0u) + (tcls == (uint32_t)c ? 1u : 0u);
+        __syncthreads();
+        s[e] = cnt;
+        __syncthreads();
+        for (uint32_t o = 1; o < 512; o <<= 1) {
+            const uint32_t v = e >= o ? s[e - o] : 0u;
+            __syncthreads();
+            s[e] += v;
+            __syncthreads();
+        }
+        const uint32_t start = base + s[e] - cnt;
+        uint32_t k = 0;
+        if (c == 3)
+            for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * MT));
+        if (tcls == (uint32_t)c && start + k < cap) tiles[start + k] = make_int2((int)e, (int)(nfull * MT));
+        __syncthreads();
+        if (e == 511) base += s[511];
+    }
     __syncthreads();
-    for (uint32_t o = 1; o < 512; o <<= 1) {
-        const uint32_t v = e >= o ? s[e - o] : 0u;
-        __syncthreads();
-        s[e] += v;
-        __syncthreads();
-    }
-    const uint32_t start = s[e] - c;
-    for (uint32_t i = 0; i < c && start + i < max_tiles; i++)
-        tiles[start + i] = make_int2((int)e, (int)(i * MT));
-    if (e == 511) *count = min(s[511], max_tiles);
+    if (e == 0) *count = min(base, cap);
 }
 
 // --------------------------------------------------------------- kernel
@@ -239,23 +258,21 @@ __device__ inline void mmq_wait(uint32_t n) {
 // workgroup barrier that leaves this kernel's copies in flight
 __device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <uint32_t TY, bool FUSED>
-__global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
+// One (expert, weight block, token tile) of NSUB 32-row token sub-tiles.
+template <uint32_t TY, bool FUSED, int NSUB>
+__device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, uint8_t *smem,
+                                                               const int2 tinfo) {
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
     constexpr uint32_t SB = RawSpec<TY>::SB;
     constexpr uint32_t SSD = RawSpec<TY>::SS / 4;             // raw slot dwords
     constexpr uint32_t RAW_OPS = (MMQ_NB * SSD + 63) / 64;    // dword copies per superblock
     constexpr uint32_t RAW_PER_WAVE = (RAW_OPS + 3) / 4;
-    constexpr uint32_t ST_OPS = 5;                            // copies per stage per wave
+    constexpr uint32_t ST_OPS = NSUB + 1;                     // copies per stage per wave
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t ti = blockIdx.y;
-    if (ti >= *a.ntiles) return;
-    const int2 tinfo = a.tiles[ti];
     const uint32_t e = (uint32_t)tinfo.x;
     const int32_t rbase = a.bounds[e] + tinfo.y;
-    const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), (uint32_t)MMQ_MB);
+    const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), 32u * NSUB);
     const uint8_t *We = a.w + (uint64_t)e * a.estride;
     // weight row (within the expert) of tile row r
     const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
@@ -286,10 +303,10 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     }
     // source rows of this lane's copies: activation op m covers tile rows
     // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
-    const _Float16 *arow_src[4];
-    bool arow_ok[4];
+    const _Float16 *arow_src[NSUB];
+    bool arow_ok[NSUB];
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 0; m < NSUB; m++) {
         const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
         arow_ok[m] = r < mrows;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
@@ -312,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     auto issue_stage = [&](uint32_t s) __attribute__((always_inline)) {
         const uint32_t buf = s & 1u;
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
+        for (int m = 0; m < NSUB; m++) {
             const uint32_t j = wv + 4 * m;            // 8 rows per op
             const uint32_t r = 8 * j + lane / 8;
             const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
@@ -345,9 +362,9 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
         }
     };
 
-    f32x16_t acc[4], inner[4];
+    f32x16_t acc[NSUB], inner[NSUB];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < NSUB; t++) {
         acc[t] = f32x16_t{};
         inner[t] = f32x16_t{};
     }
@@ -382,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
             decode_a<TY>(L, R, j, kh, A0, A1);
             const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
 #pragma unroll
-            for (int tp = 0; tp < 4; tp += MMQ_TP) {  // MMQ_TP token sub-tiles at a time
+            for (int tp = 0; tp < NSUB; tp += MMQ_TP) {  // MMQ_TP token sub-tiles at a time
                 f32x16_t sacc[MMQ_TP];
                 float dxv[MMQ_TP];
 #pragma unroll
@@ -419,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
                 const uint32_t no = (uint32_t)((uintptr_t)wsrc(n, sbi) & 3u);
                 const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][no]));
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
+                for (int t = 0; t < NSUB; t++) {
                     acc[t][i] = fmaf(inner[t][i], dw, acc[t][i]);
                     inner[t][i] = 0.f;
                 }
@@ -429,7 +446,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     if (!FUSED) {
         // lane: token column 32t + lane%32, weight rows 32wv + 8b + 4kh + 0..3
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < NSUB; t++) {
             const uint32_t p = 32 * t + (lane & 31u);
             if (p < mrows) {
                 float *o = a.dst + (uint64_t)(rbase + (int32_t)p) * a.ld + nblk + 32 * wv + 4 * kh;
@@ -446,14 +463,14 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     float *ex = (float *)&L.act[0][0][0];   // [2 waves][4 t][16 i][64 lanes] = 32 KB
     if (wv >= 2) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < NSUB; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) ex[(((wv - 2) * 4 + t) * 16 + i) * 64 + lane] = acc[t][i];
     }
     __syncthreads();
     if (wv >= 2) return;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < NSUB; t++) {
         const uint32_t p = 32 * t + (lane & 31u);
         float h[16];
         float amax = 0.f;
@@ -492,6 +509,22 @@ __global__ __launch_bounds__(256) void swiglu_k(const float *__restrict__ gu,
     const uint64_t r = i / n_ff, k = i % n_ff;
     const float g = gu[r * 2 * n_ff + k], u = gu[r * 2 * n_ff + n_ff + k];
     h[i] = g / (1.f + expf(-g)) * u;
+}
+
+template <uint32_t TY, bool FUSED>
+__global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t ti = blockIdx.y;
+    if (ti >= *a.ntiles) return;
+    const int2 tinfo = a.tiles[ti];
+    const int32_t rows = a.bounds[tinfo.x + 1] - a.bounds[tinfo.x] - tinfo.y;
+    // block-uniform choice of the (branch-free) sub-tile count
+    switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
+    case 4: mmq_tile<TY, FUSED, 4>(a, smem, tinfo); break;
+    case 3: mmq_tile<TY, FUSED, 3>(a, smem, tinfo); break;
+    case 2: mmq_tile<TY, FUSED, 2>(a, smem, tinfo); break;
+    default: mmq_tile<TY, FUSED, 1>(a, smem, tinfo); break;
+    }
 }
 
 static int2 *g_tiles = nullptr;
