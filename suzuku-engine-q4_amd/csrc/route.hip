@@ -97,83 +97,118 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
     }
 }
 
-// Stable pack of one token group per block (1024 threads = 16 waves).
-// Rounds of 1024 consecutive (t, k) entries: inside a wave, entries with
-// the same expert are found with 10 ballots (ids < 1024); a wave's offset
-// for expert e adds the counts of the earlier waves of the round and the
-// expert's running cursor, so positions follow scan order exactly.
-__global__ __launch_bounds__(1024) void assign_k(
+// ----------------------------------------------------------------- pack
+// Stable counting sort of a token group's (token, pick) rows by expert, in
+// two launches over 512-row chunks so that every chunk has its own block:
+//   pack_hist_k   per chunk: rows per expert -> hist[g][chunk][e]
+//   pack_place_k  per chunk: the expert's first position (its exclusive
+//                 prefix over experts + the counts of earlier chunks), then
+//                 each row's rank among the chunk's earlier rows of the same
+//                 expert (wave ballots on the expert id bits, then the
+//                 counts of earlier waves).  Rows keep their (t, k) order
+//                 inside an expert: the host pack's order, bit for bit.
+constexpr uint32_t kPackCh = 512;
+
+__global__ __launch_bounds__(512) void pack_hist_k(const int32_t *__restrict__ ids,
+                                                   uint32_t *__restrict__ hist, uint32_t gsz,
+                                                   uint32_t topk, uint32_t n_exp, uint32_t n_tok,
+                                                   uint32_t nch) {
+    __shared__ uint32_t h[512];
+    const uint32_t c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    h[tid] = 0;
+    __syncthreads();
+    const uint32_t t0 = g * gsz, t1 = min(t0 + gsz, n_tok);
+    const uint32_t rows = (t1 - t0) * topk;
+    const uint32_t i = c * kPackCh + tid;
+    if (i < rows) {
+        const int32_t e = ids[(size_t)t0 * topk + i];
+        if (e >= 0 && (uint32_t)e < n_exp) atomicAdd(&h[e], 1u);
+    }
+    __syncthreads();
+    hist[((size_t)g * nch + c) * 512 + tid] = h[tid];
+}
+
+// Inclusive sum over the block's 512 threads (one value each).
+__device__ inline uint32_t scan512(uint32_t v, uint32_t *tmp, uint32_t tid) {
+    tmp[tid] = v;
+    __syncthreads();
+    for (uint32_t o = 1; o < 512; o <<= 1) {
+        const uint32_t u = tid >= o ? tmp[tid - o] : 0u;
+        __syncthreads();
+        tmp[tid] += u;
+        __syncthreads();
+    }
+    const uint32_t r = tmp[tid];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(512) void pack_place_k(
     const int32_t *__restrict__ ids, const float *__restrict__ wts, int32_t *__restrict__ a_tok,
     int32_t *__restrict__ rsrc, float *__restrict__ rw, int32_t *__restrict__ stg,
     uint32_t *__restrict__ stgn, uint32_t *__restrict__ ek, int32_t *__restrict__ bounds,
-    uint32_t gsz, uint32_t topk, uint32_t n_exp, uint32_t n_tok) {
-    __shared__ uint32_t s_cnt[512];
-    __shared__ uint32_t s_cur[512];
-    __shared__ uint16_t s_wc[16][512];
-    const uint32_t g = blockIdx.x, tid = threadIdx.x;
+    const uint32_t *__restrict__ hist, uint32_t gsz, uint32_t topk, uint32_t n_exp,
+    uint32_t n_tok, uint32_t nch) {
+    __shared__ uint32_t s_base[512];
+    __shared__ uint32_t s_tmp[512];
+    __shared__ uint16_t s_wc[8][512];
+    const uint32_t c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const uint32_t wv = tid >> 6, lane = tid & 63u;
-    const uint32_t t0 = g * gsz;
-    const uint32_t t1 = min(t0 + gsz, n_tok);
+    const uint32_t t0 = g * gsz, t1 = min(t0 + gsz, n_tok);
     const uint32_t rows = (t1 - t0) * topk;
     const size_t seg = (size_t)g * gsz * topk;
-    const int32_t *gid = ids + (size_t)t0 * topk;
-    for (uint32_t i = tid; i < 512; i += 1024) s_cnt[i] = 0;
-    for (uint32_t i = tid; i < 16 * 512; i += 1024) (&s_wc[0][0])[i] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < rows; i += 1024) {
-        const int32_t e = gid[i];
-        if (e >= 0 && (uint32_t)e < n_exp) atomicAdd(&s_cnt[e], 1u);
+    // expert tid: rows in the whole group and in the chunks before this one
+    uint32_t tot = 0, before = 0;
+    const uint32_t *hg = hist + (size_t)g * nch * 512 + tid;
+    for (uint32_t c2 = 0; c2 < nch; c2++) {
+        const uint32_t v = hg[(size_t)c2 * 512];
+        tot += v;
+        before += c2 < c ? v : 0u;
     }
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t b = 0, ns = 0;
-        for (uint32_t e = 0; e < n_exp; e++) {
-            const uint32_t c = s_cnt[e];
-            s_cur[e] = b;
-            if (bounds) bounds[(size_t)g * (n_exp + 1) + e] = (int32_t)b;
-            if (c) stg[(size_t)g * 512 + ns++] = (int32_t)e;
-            b += c;
+    for (uint32_t k = tid; k < 8 * 512; k += 512) (&s_wc[0][0])[k] = 0;
+    const uint32_t incl = scan512(tot, s_tmp, tid);
+    const uint32_t ebase = incl - tot;
+    s_base[tid] = ebase + before;
+    if (c == 0) {   // group-level outputs, once
+        if (bounds) {
+            if (tid < n_exp) bounds[(size_t)g * (n_exp + 1) + tid] = (int32_t)ebase;
+            if (tid == n_exp - 1) bounds[(size_t)g * (n_exp + 1) + n_exp] = (int32_t)incl;
         }
-        if (bounds) bounds[(size_t)g * (n_exp + 1) + n_exp] = (int32_t)b;
-        stgn[g] = ns;
+        ek[(size_t)g * 512 + tid] = tid < n_exp ? tot : 0u;
     }
-    for (uint32_t i = tid; i < 512; i += 1024) ek[(size_t)g * 512 + i] = i < n_exp ? s_cnt[i] : 0;
-    __syncthreads();
-    const uint64_t lt = (1ull << lane) - 1ull;
-    for (uint32_t base = 0; base < rows; base += 1024) {
-        const uint32_t i = base + tid;
-        const bool in = i < rows;
-        const int32_t e = in ? gid[i] : -1;
-        const bool valid = in && e >= 0 && (uint32_t)e < n_exp;
-        uint64_t same = __ballot(valid);
+    // used experts in ascending order
+    const uint32_t used = (tid < n_exp && tot) ? 1u : 0u;
+    const uint32_t uincl = scan512(used, s_tmp, tid);
+    if (c == 0) {
+        if (used) stg[(size_t)g * 512 + uincl - 1] = (int32_t)tid;
+        if (tid == 511) stgn[g] = uincl;
+    }
+    // this chunk's rows, one per thread
+    const uint32_t i = c * kPackCh + tid;
+    const bool in = i < rows;
+    const int32_t e = in ? ids[(size_t)t0 * topk + i] : -1;
+    const bool valid = in && e >= 0 && (uint32_t)e < n_exp;
+    uint64_t same = __ballot(valid);
 #pragma unroll
-        for (int b = 0; b < 10; b++) {
-            const bool bit = valid && ((e >> b) & 1);
-            const uint64_t m = __ballot(bit);
-            same &= bit ? m : ~m;
-        }
-        if (!valid) same = 0;
-        const uint32_t rank = (uint32_t)__popcll(same & lt);
-        const bool leader = valid && rank == 0;
-        if (leader) s_wc[wv][e] = (uint16_t)__popcll(same);
-        __syncthreads();
-        if (valid) {
-            uint32_t p = s_cur[e] + rank;
-            for (uint32_t w2 = 0; w2 < wv; w2++) p += s_wc[w2][e];
-            const uint32_t t = t0 + i / topk;
-            a_tok[seg + p] = (int32_t)t;
-            rsrc[(size_t)t0 * topk + i] = (int32_t)p;
-            rw[(size_t)t0 * topk + i] = wts[(size_t)t0 * topk + i];
-        } else if (in) {
-            rsrc[(size_t)t0 * topk + i] = -1;
-            rw[(size_t)t0 * topk + i] = 0.f;
-        }
-        __syncthreads();
-        if (leader) {
-            atomicAdd(&s_cur[e], (uint32_t)s_wc[wv][e]);
-            s_wc[wv][e] = 0;
-        }
-        __syncthreads();
+    for (int b = 0; b < 9; b++) {
+        const bool bit = valid && ((e >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        same &= bit ? m : ~m;
+    }
+    if (!valid) same = 0;
+    const uint32_t rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+    if (valid && rank == 0) s_wc[wv][e] = (uint16_t)__popcll(same);
+    __syncthreads();
+    if (valid) {
+        uint32_t p = s_base[e] + rank;
+        for (uint32_t w2 = 0; w2 < wv; w2++) p += s_wc[w2][e];
+        const uint32_t t = t0 + i / topk;
+        a_tok[seg + p] = (int32_t)t;
+        rsrc[(size_t)t0 * topk + i] = (int32_t)p;
+        rw[(size_t)t0 * topk + i] = wts[(size_t)t0 * topk + i];
+    } else if (in) {
+        rsrc[(size_t)t0 * topk + i] = -1;
+        rw[(size_t)t0 * topk + i] = 0.f;
     }
 }
 
@@ -213,13 +248,34 @@ bool route_launch(const float *lg, int32_t *ids, float *wts, uint32_t n_tok, uin
     return launch_ok("route_k");
 }
 
+// per-chunk expert histograms of the pack (library scratch; grown on demand,
+// so a caller that captures graphs runs one pack of its largest size first)
+static uint32_t *g_hist = nullptr;
+static size_t g_hist_words = 0;
+
 bool assign_launch(const int32_t *ids, const float *wts, int32_t *a_tok, int32_t *rsrc,
                    float *rw, int32_t *stg, uint32_t *stgn, uint32_t *ek, int32_t *bounds,
                    uint32_t gsz, uint32_t topk, uint32_t n_exp, uint32_t n_tok) {
     const uint32_t n_g = (n_tok + gsz - 1) / gsz;
-    assign_k<<<dim3(n_g), dim3(1024), 0, stream()>>>(ids, wts, a_tok, rsrc, rw, stg, stgn, ek,
-                                                    bounds, gsz, topk, n_exp, n_tok);
-    return launch_ok("assign_k");
+    const uint32_t nch = (gsz * topk + kPackCh - 1) / kPackCh;
+    const size_t words = (size_t)n_g * nch * 512;
+    if (g_hist_words < words) {
+        uint32_t *n = nullptr;
+        if (hipMalloc(&n, words * 4) != hipSuccess) {
+            set_error("pack: scratch allocation failed");
+            return false;
+        }
+        if (g_hist) (void)hipFree(g_hist);
+        g_hist = n;
+        g_hist_words = words;
+    }
+    pack_hist_k<<<dim3(nch, n_g), dim3(512), 0, stream()>>>(ids, g_hist, gsz, topk, n_exp, n_tok,
+                                                           nch);
+    if (!launch_ok("pack_hist_k")) return false;
+    pack_place_k<<<dim3(nch, n_g), dim3(512), 0, stream()>>>(ids, wts, a_tok, rsrc, rw, stg, stgn,
+                                                            ek, bounds, g_hist, gsz, topk, n_exp,
+                                                            n_tok, nch);
+    return launch_ok("pack_place_k");
 }
 
 bool reduce_launch(float *dy, const float *pd, const int32_t *rsrc, const float *rw,
