@@ -121,9 +121,9 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
 // 0,1 through LDS, which form h = silu(g)*u and write its q8 codes (the
 // 32 h columns of a q8 group are in the lane and its partner lane l^32).
 constexpr int MMQ_NB = 128;      // weight rows per block
-#ifndef MMQ_TP
-#define MMQ_TP 1                 // token sub-tiles whose MFMA chains overlap
-#endif
+// token sub-tiles whose MFMA chains are interleaved (two measured no faster
+// than one, and one keeps the register budget clear of spills)
+template <bool FUSED> constexpr int mmq_tp() { return 1; }
 constexpr int MMQ_MB = 128;      // token rows per block
 
 template <uint32_t TY>
@@ -398,12 +398,13 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             half8_t A0, A1;
             decode_a<TY>(L, R, j, kh, A0, A1);
             const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
+            constexpr int TP = (NSUB % 2 == 0) ? mmq_tp<FUSED>() : 1;
 #pragma unroll
-            for (int tp = 0; tp < NSUB; tp += MMQ_TP) {  // MMQ_TP token sub-tiles at a time
-                f32x16_t sacc[MMQ_TP];
-                float dxv[MMQ_TP];
+            for (int tp = 0; tp < NSUB; tp += TP) {   // TP token sub-tiles at a time
+                f32x16_t sacc[TP];
+                float dxv[TP];
 #pragma unroll
-                for (int u = 0; u < MMQ_TP; u++) {
+                for (int u = 0; u < TP; u++) {
                     const uint32_t tok = 32 * (tp + u) + (lane & 31u);
                     const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
                     const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
@@ -412,7 +413,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
                     dxv[u] = L.dx[buf][tok][gl];
                 }
 #pragma unroll
-                for (int u = 0; u < MMQ_TP; u++) {
+                for (int u = 0; u < TP; u++) {
                     const int t = tp + u;
                     if (TY == Q4MI_T_IQ3_S) {
 #pragma unroll
