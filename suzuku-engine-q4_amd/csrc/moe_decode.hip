@@ -868,7 +868,7 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
         S = fixed < kLdsCap ? (uint32_t)std::min<size_t>(kMaxS, (kLdsCap - fixed) / slot) : 0;
         if (S >= 2 || ch == 1) break;
     }
-    // a consumer wave's four items touch at most two chunks (ch * kDnRows >= 8)
+    // a consumer wave's 64/TPR (<= 8) consecutive items touch at most two chunks (ch * kDnRows >= 8)
     const uint32_t C = (nu_est + ch - 1) / ch;
     if (S < 2 && S < C) {
         set_error("moe_dn_k: LDS limit");
@@ -916,12 +916,21 @@ static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
     return false;
 }
 
+// Down lanes per item: 8 lanes with two groups each for 16-group rows, so
+// 96 teams cover a block's (expert, row) items in one round; else the row
+// layout.
+static RowLayout dn_layout(uint32_t G, int NT) {
+    if (G == 16 && NT <= 2) return RowLayout{8, 2};
+    return layout_for(G);
+}
+
 template <uint32_t TY, int NT>
 static bool dn_dispatch(const MoeArgs &a, uint32_t nu_host) {
-    const RowLayout L = layout_for(a.n_ff / 32);
+    const RowLayout L = dn_layout(a.n_ff / 32, NT);
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_dn<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+    if constexpr (NT <= 2) { Q4MI_L(8, 2) }
 #undef Q4MI_L
     return false;
 }
