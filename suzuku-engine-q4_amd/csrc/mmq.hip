@@ -70,12 +70,18 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 // sub-tiles, so a tail of a few rows costs a 32-row tile, not a 128-row
 // one.  The list is ordered by tile size, largest first (longest work is
 // scheduled first).
+//
+// One block, thread e = expert e.  The four classes' tile counts of an
+// expert are packed into one 64-bit word (16 bits per class, class 3 = the
+// 128-row class in the top field), so a single exclusive scan over the
+// experts gives every class's offsets at once: a wave scan, then one step
+// across the 8 waves.  Field sums stay below 2^16 (at most
+// total_rows/128 + n_exp <= 65535 tiles, checked by the caller).
 __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ bounds,
                                                    uint32_t n_exp, int2 *__restrict__ tiles,
                                                    uint32_t *__restrict__ count, uint32_t cap) {
-    __shared__ uint32_t s[512];
-    __shared__ uint32_t base;
-    const uint32_t e = threadIdx.x;
+    __shared__ uint64_t wsum[8];
+    const uint32_t e = threadIdx.x, lane = e & 63u, w = e >> 6;
     uint32_t n = 0;
     if (e < n_exp) {
         const int32_t v = bounds[e + 1] - bounds[e];
@@ -83,28 +89,41 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
     }
     const uint32_t nfull = n / MT, tail = n % MT;
     const uint32_t tcls = tail ? (tail + 31) / 32 - 1 : 4u;   // 4 = no tail tile
-    if (e == 0) base = 0;
-    for (int c = 3; c >= 0; c--) {
-        const uint32_t cnt = (c == 3 ? nfull : 0u) + (tcls == (uint32_t)c ? 1u : 0u);
-        __syncthreads();
-        s[e] = cnt;
-        __syncthreads();
-        for (uint32_t o = 1; o < 512; o <<= 1) {
-            const uint32_t v = e >= o ? s[e - o] : 0u;
-            __syncthreads();
-            s[e] += v;
-            __syncthreads();
-        }
-        const uint32_t start = base + s[e] - cnt;
-        uint32_t k = 0;
-        if (c == 3)
-            for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * MT));
-        if (tcls == (uint32_t)c && start + k < cap) tiles[start + k] = make_int2((int)e, (int)(nfull * MT));
-        __syncthreads();
-        if (e == 511) base += s[511];
+    auto field = [](uint32_t c) { return 16u * c; };
+    uint64_t mine = (uint64_t)nfull << field(3);
+    if (tcls < 4) mine += 1ull << field(tcls);
+    uint64_t incl = mine;
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint64_t v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
     }
+    if (lane == 63) wsum[w] = incl;
     __syncthreads();
-    if (e == 0) *count = min(base, cap);
+    uint64_t before = 0, total = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) {
+        const uint64_t v = wsum[k];
+        if (k < w) before += v;
+        total += v;
+    }
+    const uint64_t excl = before + incl - mine;
+    auto get = [&](uint64_t v, uint32_t c) { return (uint32_t)(v >> field(c)) & 0xFFFFu; };
+    // classes laid out largest first: 3, 2, 1, 0
+    uint32_t cbase[4];
+    cbase[3] = 0;
+    cbase[2] = get(total, 3);
+    cbase[1] = cbase[2] + get(total, 2);
+    cbase[0] = cbase[1] + get(total, 1);
+    const uint32_t all = cbase[0] + get(total, 0);
+    uint32_t start = cbase[3] + get(excl, 3);
+    uint32_t k = 0;
+    for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * MT));
+    if (tcls < 4) {
+        const uint32_t at = tcls == 3 ? start + nfull : cbase[tcls] + get(excl, tcls);
+        if (at < cap) tiles[at] = make_int2((int)e, (int)(nfull * MT));
+    }
+    if (e == 0) *count = min(all, cap);
 }
 
 // --------------------------------------------------------------- kernel
