@@ -478,37 +478,52 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         }
         return;
     }
-    // fused: waves 2,3 (up rows) hand their accumulators to waves 0,1
+    // fused: wave w < 2 holds gate rows 32w..32w+31 of h's columns, wave
+    // w + 2 the matching up rows.  The pair splits the token sub-tiles: the
+    // gate wave forms h for t < TS, the up wave for t >= TS, each taking the
+    // other half's accumulators through LDS.
+    constexpr int TS = (NSUB + 1) / 2;
     __syncthreads();
-    float *ex = (float *)&L.act[0][0][0];   // [2 waves][4 t][16 i][64 lanes] = 32 KB
-    if (wv >= 2) {
-#pragma unroll
-        for (int t = 0; t < NSUB; t++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) ex[(((wv - 2) * 4 + t) * 16 + i) * 64 + lane] = acc[t][i];
-    }
-    __syncthreads();
-    if (wv >= 2) return;
+    // [4 waves][2 slots][16 i][64 lanes] = 32 KB; sub-tile t uses slot
+    // t < TS ? t : t - TS (a wave hands over at most two sub-tiles)
+    float *ex = (float *)&L.act[0][0][0];
+    static_assert(sizeof(MmqLds<TY>::act) >= 4 * 2 * 16 * 64 * sizeof(float), "hand-off space");
+    auto slot = [&](int t) { return t < TS ? t : t - TS; };
+    const bool gate_w = wv < 2;
 #pragma unroll
     for (int t = 0; t < NSUB; t++) {
+        if ((t < TS) != gate_w) {           // the half the partner wave finishes
+#pragma unroll
+            for (int i = 0; i < 16; i++) ex[((wv * 2 + slot(t)) * 16 + i) * 64 + lane] = acc[t][i];
+        }
+    }
+    __syncthreads();
+    const uint32_t pw = wv ^ 2u;            // partner wave
+    const uint32_t col = 32 * (wv & 1u);    // h columns of this pair: col + 0..31
+#pragma unroll
+    for (int t = 0; t < NSUB; t++) {
+        if ((t < TS) != gate_w) continue;
         const uint32_t p = 32 * t + (lane & 31u);
         float h[16];
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float g = acc[t][i];
-            const float u = ex[((wv * 4 + t) * 16 + i) * 64 + lane];
-            h[i] = g / (1.f + expf(-g)) * u;
+            const float other = ex[((pw * 2 + slot(t)) * 16 + i) * 64 + lane];
+            const float g = gate_w ? acc[t][i] : other;
+            const float u = gate_w ? other : acc[t][i];
+            // silu(g) * u with the hardware exp2 / reciprocal (a few ulp of
+            // h; the q8 scale below stays correctly rounded)
+            h[i] = g * u * __builtin_amdgcn_rcpf(1.f + __expf(-g));
             amax = fmaxf(amax, fabsf(h[i]));
         }
-        // the q8 group = h columns 32wv + 0..31 of token p: this lane has
+        // the q8 group = h columns col + 0..31 of token p: this lane has
         // columns 8b + 4kh + 0..3, the partner lane (lane ^ 32) the rest
         amax = fmaxf(amax, __shfl_xor(amax, 32));
         const float d = __fdiv_rn(amax, 127.f);
         const float sc = amax > 0.f ? __fdiv_rn(127.f, amax) : 0.f;
         if (p < mrows) {
             const uint64_t prow = (uint64_t)(rbase + (int32_t)p);
-            _Float16 *o = a.hq + prow * a.n_ff + nblk + 32 * wv + 4 * kh;
+            _Float16 *o = a.hq + prow * a.n_ff + nblk + col + 4 * kh;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 half4_t v;
@@ -516,7 +531,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
                 for (int c = 0; c < 4; c++) v[c] = (_Float16)(float)q4mi_q8_code(h[4 * b + c] * sc);
                 *(half4_t *)(o + 8 * b) = v;
             }
-            if (kh == 0) a.hd[prow * (a.n_ff / 32) + (nblk + 32 * wv) / 32] = d;
+            if (kh == 0) a.hd[prow * (a.n_ff / 32) + (nblk + col) / 32] = d;
         }
     }
 }
