@@ -145,12 +145,18 @@ constexpr int MMQ_NB = 128;      // weight rows per block
 template <bool FUSED> constexpr int mmq_tp() { return 1; }
 constexpr int MMQ_MB = 128;      // token rows per block
 
+// Raw superblock slots in LDS.  A row's slot holds the dwords covering its
+// superblock, which starts 0 or 2 bytes into a dword (rows are 4-byte
+// multiples, so the offset is the same for every row of a tile).
+//   IQ3_S: 28 data dwords + 1 pad = 29 per row.  29 is odd, so the 32 rows
+//          one wave decodes at a common byte offset fall on 32 banks, and
+//          one 58-lane copy fills two whole rows.
+//   Q8_0:  the dwords rounded to an even count, copied as one linear run.
 template <uint32_t TY>
 struct RawSpec {
     static constexpr uint32_t SB = TY == Q4MI_T_IQ3_S ? 110u : 8u * 34u;  // bytes / 256 values
-    // LDS slot: the dwords covering a superblock that starts 0 or 2 bytes into
-    // a dword, rounded to an even count (two staging threads per row)
-    static constexpr uint32_t SS = ((SB + 2u + 3u) / 4u + 1u) / 2u * 8u;
+    static constexpr uint32_t SS = TY == Q4MI_T_IQ3_S ? 29u * 4u
+                                                      : ((SB + 2u + 3u) / 4u + 1u) / 2u * 8u;
 };
 
 // Double-buffered stages of 64 K values (two q8 groups).  Activation rows
@@ -284,7 +290,9 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
     constexpr uint32_t SB = RawSpec<TY>::SB;
     constexpr uint32_t SSD = RawSpec<TY>::SS / 4;             // raw slot dwords
-    constexpr uint32_t RAW_OPS = (MMQ_NB * SSD + 63) / 64;    // dword copies per superblock
+    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
+    // dword copies per superblock: IQ3_S two rows per copy, else linear
+    constexpr uint32_t RAW_OPS = kIq ? MMQ_NB / 2 : (MMQ_NB * SSD + 63) / 64;
     constexpr uint32_t RAW_PER_WAVE = (RAW_OPS + 3) / 4;
     constexpr uint32_t ST_OPS = NSUB + 1;                     // copies per stage per wave
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
@@ -361,9 +369,25 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
     };
     // copies of superblock sbi's raw weight bytes into buffer sbi & 1
+    // IQ3_S copy lanes: lane < 29 -> dword `lane` of the first row, 29..57 ->
+    // dword lane-29 of the second row (the pad dword re-reads dword 27)
+    const uint32_t rsel = lane >= 29u ? 1u : 0u;
+    const uint32_t lofs = rsel * a.rb + 4u * min(lane - 29u * rsel, 27u);
     auto issue_raw = [&](uint32_t sbi) __attribute__((always_inline)) {
         const uint32_t buf = sbi & 1u;
         uint8_t *base = &L.raw[buf][0][0];
+        if constexpr (kIq) {
+            // rows 2j, 2j+1 are adjacent in memory (gate/up halves split at
+            // an even row): one wave-uniform base per copy
+            const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);
+#pragma unroll
+            for (uint32_t m = 0; m < RAW_PER_WAVE; m++) {
+                const uint32_t j = wv + 4 * m;
+                const uint8_t *rb0 = wsrc(2 * j, sbi) - roff;
+                if (lane < 58u) mmq_copy<4>(rb0 + lofs, mmq_lds(base + 2u * j * RawSpec<TY>::SS));
+            }
+            return;
+        }
 #pragma unroll
         for (uint32_t m = 0; m < RAW_PER_WAVE; m++) {
             const uint32_t j = wv + 4 * m;
@@ -409,7 +433,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         const uint32_t buf = s & 1u;
         // the row's raw bytes start at the same offset inside its slot as
         // in memory (the slot begins at the enclosing dword)
-        const uint32_t roff = (uint32_t)((uintptr_t)wsrc(arow, sbi) & 3u);
+        const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);   // same for every row
         const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
 #pragma unroll
         for (int gl = 0; gl < 2; gl++) {
@@ -441,8 +465,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
 #pragma unroll
                         for (int i = 0; i < 16; i++) {
                             const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                            const uint32_t no = (uint32_t)((uintptr_t)wsrc(n, sbi) & 3u);
-                            const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][no] + 34 * j));
+                            const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][roff] + 34 * j));
                             acc[t][i] = fmaf(sacc[u][i], dxv[u] * dw, acc[t][i]);
                         }
                     }
@@ -453,8 +476,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                const uint32_t no = (uint32_t)((uintptr_t)wsrc(n, sbi) & 3u);
-                const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][no]));
+                const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][roff]));
 #pragma unroll
                 for (int t = 0; t < NSUB; t++) {
                     acc[t][i] = fmaf(inner[t][i], dw, acc[t][i]);
@@ -581,8 +603,9 @@ static bool ensure_tiles(uint32_t n) {
 
 bool mmq_supported(uint32_t ty, uint64_t w_rows, uint64_t w_cols) {
     if (ty != Q4MI_T_IQ3_S && ty != Q4MI_T_Q8_0) return false;
+    // rows must be 4-byte multiples (IQ3_S: an even number of superblocks)
     return w_rows > 0 && w_rows % MMQ_NB == 0 && w_cols > 0 && w_cols % 256 == 0 &&
-           w_cols <= 65536;
+           w_cols <= 65536 && q4mi_row_bytes(ty, w_cols) % 4 == 0;
 }
 
 bool mmq_quant(const float *x, const int32_t *ids, void *xq, uint64_t cols, uint64_t rows) {

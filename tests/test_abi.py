@@ -60,6 +60,9 @@ def test_loads_and_rejects_without_gpu():
     assert not L.q4_mmq_supported(12, 1024)
     assert L.q4_mmq_q8_bytes(10, 2048) == 10 * 2048 * 2 + 10 * 64 * 4 + 256
     assert not L.q4_mmq_mul_id(1, q4mi.T_IQ3_S, 1000, 2048, 0, 8, 16, 1, 0, 10, 16, 1000)
+    # IQ3_S rows must be whole dwords (an even number of 110-byte superblocks)
+    assert not L.q4_mmq_mul_id(16, q4mi.T_IQ3_S, 1024, 256, 0, 8, 16, 16, 0, 10, 16, 1024)
+    assert "not covered" in q4mi.last_error()
     ids = (ctypes.c_int32 * 65)()
     w = (ctypes.c_float * 65)()
     # 65 experts exceeds the per-call bound (src/q4_test.c:1652-1663)

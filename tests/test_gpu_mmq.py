@@ -72,11 +72,38 @@ def test_mul_id_ragged(gpu, oracle, ty, N, K):
         assert rel_err(dst[bounds[e]:bounds[e + 1]], ref) <= TOL, e
 
 
+@pytest.mark.parametrize("ty", [T_IQ3_S, T_Q8_0])
+def test_mul_id_misaligned_experts(gpu, oracle, ty):
+    """Expert bases 2 bytes into a dword (stride = matrix bytes + 2): every
+    superblock then starts at the other in-dword offset."""
+    rng = np.random.default_rng(17 + ty)
+    N, K, E = 256, 1024, 3
+    per = [37, 130, 5]
+    rb = om.row_bytes(ty, K)
+    W = synth.matrix(rng, ty, E * N, K)
+    estride = N * rb + 2
+    buf = np.zeros(E * estride + 8, np.uint8)
+    for e in range(E):
+        buf[e * estride:e * estride + N * rb] = W[e * N * rb:(e + 1) * N * rb]
+    T = 200
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    a_tok = np.concatenate([rng.integers(0, T, n) for n in per]).astype(np.int32)
+    bounds = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+    total = int(bounds[-1])
+    xq = mmq_quant(gpu, dev(x), dev(a_tok), K, total)
+    dst = host(mul_id(gpu, dev(buf), ty, N, K, estride, E, xq, dev(bounds), total, N))
+    for e in range(E):
+        rows = a_tok[bounds[e]:bounds[e + 1]]
+        ref = oracle.dot8_rows(ty, W[e * N * rb:(e + 1) * N * rb], N, K, x[rows])
+        assert rel_err(dst[bounds[e]:bounds[e + 1]], ref) <= TOL, e
+
+
 def test_mmq_group_sums_exact(gpu, oracle):
-    """With d_w = 1 and one activation group of d_x = 1/127 scale... the MMQ
-    output of a single 256-value row equals the oracle's exact integer sums."""
+    """With d_w = 1 and activations whose q8 scale is exactly 1, the MMQ
+    output of each 512-value row equals the oracle's exact integer sums."""
     rng = np.random.default_rng(77)
-    N, K = 128, 256
+    N, K = 128, 512
+    rb = om.row_bytes(T_IQ3_S, K)
     W = synth.matrix(rng, T_IQ3_S, N, K)
     Wb = W.reshape(-1, 110)
     Wb[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
@@ -85,12 +112,12 @@ def test_mmq_group_sums_exact(gpu, oracle):
     bounds = np.array([0, 3], np.int32)
     dx, dW, dbounds = dev(x), dev(W), dev(bounds)
     xq = mmq_quant(gpu, dx, None, K, 3)
-    dst = host(mul_id(gpu, dW, T_IQ3_S, N, K, N * 110, 1, xq, dbounds, 3, N))
+    dst = host(mul_id(gpu, dW, T_IQ3_S, N, K, N * rb, 1, xq, dbounds, 3, N))
     for t in range(3):
         q, d, _ = oracle.quant8(x[t])
         assert np.all(d == 1.0) and np.array_equal(q.astype(np.float32), x[t])
         for n in range(N):
-            s = oracle.group_sums(T_IQ3_S, W[n * 110:(n + 1) * 110], K, q)
+            s = oracle.group_sums(T_IQ3_S, W[n * rb:(n + 1) * rb], K, q)
             assert dst[t, n] == float(s.sum())
 
 
