@@ -711,9 +711,16 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     const uint32_t cw = wave - kProd;
     // y of this block's rows and the host list's weights (needed at the end;
     // loaded now, weight u in lane u)
+    // (output o = (t, rr) is summed by the 8 lanes 8o..8o+7; the last one
+    // adds the old y and stores)
     float yv = 0.f;
-    if (ct < nt * nr) yv = a.y[(size_t)(ct / nr) * a.n_embd + r0 + ct % nr];
+    if ((ct & 7u) == 7u && (ct >> 3) < nt * nr) {
+        const uint32_t o = ct >> 3;
+        yv = a.y[(size_t)(o / nr) * a.n_embd + r0 + o % nr];
+    }
     const float wv = __builtin_bit_cast(float, hword);
+    // host list: its weights go to Plan::w[0] for the final sum
+    if (uniq && cw == 0 && lane < nu) P->w[0][lane] = wv;
     // q8 of every selected h row; pair slot s holds h[u][t] (slots of u are
     // its selected tokens in order).  Every prologue load is issued before
     // any is used.
@@ -790,19 +797,16 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     if (lane == 0) atomicAdd(&Y->fin, 1u);
     spin_ge(&Y->fin, kConsW);                       // every partial sum written
     Q4MI_TR(29, 1, ct == 0);
-    // y[t][r] += sum_u w[u][t] * part[u][t][r], u in plan order
-    if (ct < nt * nr) {
-        const uint32_t t = ct / nr, rr = ct % nr;
+    // y[t][r] += sum_u w[u][t] * part[u][t][r]: lane sl of an output's
+    // 8 lanes takes experts u = sl, sl + 8, ... in plan order, then a fixed
+    // DPP tree joins the 8 partial sums (deterministic)
+    if (ct < 8 * nt * nr) {
+        const uint32_t o = ct >> 3, sl = ct & 7u, t = o / nr, rr = o % nr;
         float s = 0.f;
-        if (uniq) {
-            for (uint32_t u = 0; u < nu; u++)
-                s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), u)) *
-                     part[(size_t)u * NT * kDnRows + rr];
-        } else {
-            for (uint32_t u = 0; u < nu; u++)
-                if ((P->sel[u] >> t) & 1u) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
-        }
-        a.y[(size_t)t * a.n_embd + r0 + rr] = yv + s;
+        for (uint32_t u = sl; u < nu; u += 8)
+            if (uniq || ((P->sel[u] >> t) & 1u)) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
+        s = rsum<8>(s);
+        if (sl == 7u) a.y[(size_t)t * a.n_embd + r0 + rr] = yv + s;
     }
     Q4MI_TR(30, 1, ct == 0);
 }
