@@ -536,6 +536,17 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     const bool uniq = a.src.unique != 0;
     // the host list's ids, loaded while the block starts up (lane u: id u)
     const int32_t hid = (uniq && wave < kProd) ? host_ids(ka, a.src.n_fixed) : -1;
+    // consumers issue their prologue loads (codebook entry, first x quad)
+    // as their wave starts, ahead of the weight stream the producers begin
+    // after the barrier
+    const uint32_t nq = nt * K / 4;
+    uint32_t code = 0u;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (wave >= kProd) {
+        const uint32_t c0 = tid - kProd * 64;
+        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
+        if (c0 < nq) v0 = ((const float4 *)a.x)[c0];
+    }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
     if (!uniq && tid < 64) build_plan(P, a.src, tid);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -577,11 +588,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     // ---- consumers
     const uint32_t ct = tid - kProd * 64;
     const uint32_t cw = wave - kProd;               // consumer wave
-    // every prologue load is issued before any is used
-    const uint32_t nq = nt * K / 4;
     const float4 *xg = (const float4 *)a.x;
-    const uint32_t code = (kIq && ct < 512) ? q4mi_iq3s_code_dev[ct] : 0u;
-    const float4 v0 = ct < nq ? xg[ct] : make_float4(0.f, 0.f, 0.f, 0.f);
     if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, xq, xd);
     for (uint32_t i = ct + kCons; i < nq; i += kCons) quant_quad(xg[i], i, xq, xd);
@@ -676,6 +683,31 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     // the block starts up (lane u: entry u)
     const int32_t hword = !uniq ? 0 : wave < kProd ? host_ids(ka, a.src.n_fixed)
                                                   : __builtin_bit_cast(int32_t, host_weights(ka, a.src.n_fixed));
+    // consumers issue their prologue loads (codebook entry, y, and for a
+    // host list the first h quads) as their wave starts, ahead of the weight
+    // stream the producers begin after the barrier
+    const uint32_t qpr = n_ff / 4;
+    uint32_t code = 0u;
+    float yv = 0.f;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (wave >= kProd) {
+        const uint32_t c0 = tid - kProd * 64;
+        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
+        // (output o = (t, rr) is summed by the 8 lanes 8o..8o+7; the last
+        // one adds the old y and stores)
+        if ((c0 & 7u) == 7u && (c0 >> 3) < nt * nr) {
+            const uint32_t o = c0 >> 3;
+            yv = a.y[(size_t)(o / nr) * a.n_embd + r0 + o % nr];
+        }
+        if (uniq) {   // pair slot s = h row s * kMaxT
+            const uint32_t nq0 = a.src.n_fixed * qpr;
+            auto hq0 = [&](uint32_t i) {
+                return ((const float4 *)(a.h + (size_t)(i / qpr) * kMaxT * n_ff))[i % qpr];
+            };
+            if (c0 < nq0) v0 = hq0(c0);
+            if (c0 + kCons < nq0) v1 = hq0(c0 + kCons);
+        }
+    }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
     if (!uniq && tid < 64) build_plan(P, a.src, tid);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -711,28 +743,22 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     const uint32_t cw = wave - kProd;
     // y of this block's rows and the host list's weights (needed at the end;
     // loaded now, weight u in lane u)
-    // (output o = (t, rr) is summed by the 8 lanes 8o..8o+7; the last one
-    // adds the old y and stores)
-    float yv = 0.f;
-    if ((ct & 7u) == 7u && (ct >> 3) < nt * nr) {
-        const uint32_t o = ct >> 3;
-        yv = a.y[(size_t)(o / nr) * a.n_embd + r0 + o % nr];
-    }
     const float wv = __builtin_bit_cast(float, hword);
     // host list: its weights go to Plan::w[0] for the final sum
     if (uniq && cw == 0 && lane < nu) P->w[0][lane] = wv;
     // q8 of every selected h row; pair slot s holds h[u][t] (slots of u are
     // its selected tokens in order).  Every prologue load is issued before
     // any is used.
-    const uint32_t qpr = n_ff / 4, nq = nsel * qpr;
+    const uint32_t nq = nsel * qpr;
     auto hquad = [&](uint32_t i) -> const float4 * {
         const uint32_t s = i / qpr;
         const uint32_t row = uniq ? s * kMaxT : P->prow[s];
         return (const float4 *)(hg + (size_t)row * n_ff) + i % qpr;
     };
-    const uint32_t code = (kIq && ct < 512) ? q4mi_iq3s_code_dev[ct] : 0u;
-    const float4 v0 = ct < nq ? *hquad(ct) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 v1 = ct + kCons < nq ? *hquad(ct + kCons) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!uniq) {    // device list: the rows come from the plan
+        if (ct < nq) v0 = *hquad(ct);
+        if (ct + kCons < nq) v1 = *hquad(ct + kCons);
+    }
     if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, hq, hd);
     if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
