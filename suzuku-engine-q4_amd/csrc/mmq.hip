@@ -34,7 +34,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace q4mi {
 
-constexpr int MT = 128;         // token rows per tile (the tile list's granularity)
+constexpr int MT = 128;         // largest tile height (token rows); a call may use 64 or 32
 
 // ------------------------------------------------------------ quantizer
 // MMQ activation buffer layout: codes as fp16 [rows][cols], then fp32 group
@@ -76,9 +76,11 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 // 128-row class in the top field), so a single exclusive scan over the
 // experts gives every class's offsets at once: a wave scan, then one step
 // across the 8 waves.  Field sums stay below 2^16 (at most
-// total_rows/128 + n_exp <= 65535 tiles, checked by the caller).
+// total_rows/mt + n_exp <= 65535 tiles, checked by the caller).  mt (128,
+// 64 or 32) is the tile height: whole tiles are mt rows (class mt/32 - 1).
 __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ bounds,
-                                                   uint32_t n_exp, int2 *__restrict__ tiles,
+                                                   uint32_t n_exp, uint32_t mt,
+                                                   int2 *__restrict__ tiles,
                                                    uint32_t *__restrict__ count, uint32_t cap) {
     __shared__ uint64_t wsum[8];
     const uint32_t e = threadIdx.x, lane = e & 63u, w = e >> 6;
@@ -87,10 +89,10 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
         const int32_t v = bounds[e + 1] - bounds[e];
         n = v > 0 ? (uint32_t)v : 0u;
     }
-    const uint32_t nfull = n / MT, tail = n % MT;
+    const uint32_t nfull = n / mt, tail = n % mt, fcls = mt / 32 - 1;
     const uint32_t tcls = tail ? (tail + 31) / 32 - 1 : 4u;   // 4 = no tail tile
     auto field = [](uint32_t c) { return 16u * c; };
-    uint64_t mine = (uint64_t)nfull << field(3);
+    uint64_t mine = (uint64_t)nfull << field(fcls);
     if (tcls < 4) mine += 1ull << field(tcls);
     uint64_t incl = mine;
 #pragma unroll
@@ -116,12 +118,12 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
     cbase[1] = cbase[2] + get(total, 2);
     cbase[0] = cbase[1] + get(total, 1);
     const uint32_t all = cbase[0] + get(total, 0);
-    uint32_t start = cbase[3] + get(excl, 3);
+    uint32_t start = cbase[fcls] + get(excl, fcls);
     uint32_t k = 0;
-    for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * MT));
+    for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * mt));
     if (tcls < 4) {
-        const uint32_t at = tcls == 3 ? start + nfull : cbase[tcls] + get(excl, tcls);
-        if (at < cap) tiles[at] = make_int2((int)e, (int)(nfull * MT));
+        const uint32_t at = tcls == fcls ? start + nfull : cbase[tcls] + get(excl, tcls);
+        if (at < cap) tiles[at] = make_int2((int)e, (int)(nfull * mt));
     }
     if (e == 0) *count = min(all, cap);
 }
@@ -185,6 +187,7 @@ struct MmqArgs {
     const int32_t *bounds;  // [n_exp+1]
     const int2 *tiles;
     const uint32_t *ntiles;
+    uint32_t mt;            // tile height (token rows): 128, 64 or 32
     float *dst;             // plain mode: [rows][ld]
     uint64_t ld;
     _Float16 *hq;           // fused mode: [rows][n_ff] fp16 codes of h
@@ -574,7 +577,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     const uint32_t ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int2 tinfo = a.tiles[ti];
-    const int32_t rows = a.bounds[tinfo.x + 1] - a.bounds[tinfo.x] - tinfo.y;
+    const int32_t rows = min(a.bounds[tinfo.x + 1] - a.bounds[tinfo.x] - tinfo.y, (int32_t)a.mt);
     // block-uniform choice of the (branch-free) sub-tile count
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
     case 4: mmq_tile<TY, FUSED, 4>(a, smem, tinfo); break;
@@ -647,7 +650,14 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
              const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq) {
     if (!total_rows) return true;
-    const uint32_t max_tiles = (uint32_t)(total_rows / MT + n_exp + 1);
+    // tile height: the largest of 128, 64, 32 rows whose block count (from
+    // the whole-tile lower bound) still fills two blocks per CU.  Small
+    // calls (one shared expert over a prompt) trade sub-tile reuse of the
+    // weight decode for using the whole chip.
+    const uint64_t colblocks = hq ? w_rows / 2 / 64 : w_rows / MMQ_NB;
+    uint32_t mt = MT;
+    while (mt > 32 && colblocks * ((total_rows + mt - 1) / mt) < 2ull * (uint64_t)cu_count()) mt /= 2;
+    const uint32_t max_tiles = (uint32_t)(total_rows / mt + n_exp + 1);
     if (max_tiles > 65535) {
         set_error("mmq: too many row tiles (%u)", max_tiles);
         return false;
@@ -656,7 +666,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
         set_error("mmq: tile buffer allocation failed");
         return false;
     }
-    mmq_tiles_k<<<1, 512, 0, stream()>>>(bounds, n_exp, g_tiles, g_ntiles, max_tiles);
+    mmq_tiles_k<<<1, 512, 0, stream()>>>(bounds, n_exp, mt, g_tiles, g_ntiles, max_tiles);
     if (!launch_ok("mmq_tiles_k")) return false;
     MmqArgs a;
     a.w = w;
@@ -670,6 +680,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.bounds = bounds;
     a.tiles = g_tiles;
     a.ntiles = g_ntiles;
+    a.mt = mt;
     a.dst = dst;
     a.ld = ld;
     a.hq = (_Float16 *)hq;
