@@ -41,7 +41,10 @@ namespace q4mi {
 
 constexpr uint32_t kMaxU = 64;    // unique experts per call (reference bound n<=64)
 constexpr uint32_t kMaxT = 8;     // tokens per call
-constexpr uint32_t kT = 1024;     // threads per block
+#ifndef Q4MI_THREADS
+#define Q4MI_THREADS 1024
+#endif
+constexpr uint32_t kT = Q4MI_THREADS;   // threads per block
 #ifndef Q4MI_PROD
 #define Q4MI_PROD 4
 #endif
@@ -259,12 +262,11 @@ __device__ inline uint32_t dma1(uint8_t *dst, const uint8_t *src, uint32_t bytes
 }
 
 // Signed IQ3_S table in LDS, built by the consumer threads from the
-// 512-entry codebook.
-// Thread ct < 512 owns codebook entry ct (`c`, loaded by the caller).
+// 512-entry codebook.  Thread ct owns entries ct, ct + kCons, ... (the first
+// one's code `c` loaded by the caller).
 __device__ inline void build_stab(uint32_t *stab, uint32_t c, uint32_t ct) {
-    static_assert(kCons >= 512, "one codebook entry per consumer thread");
-    if (ct < 512) {
-        const uint32_t i = ct;
+    for (uint32_t i = ct; i < 512; i += kCons) {
+        if (i != ct) c = q4mi_iq3s_code_dev[i];
         uint32_t g = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) g |= (2u * ((c >> (3 * j)) & 7u) + 1u) << (8 * j);
@@ -826,13 +828,15 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     // y[t][r] += sum_u w[u][t] * part[u][t][r]: lane sl of an output's
     // 8 lanes takes experts u = sl, sl + 8, ... in plan order, then a fixed
     // DPP tree joins the 8 partial sums (deterministic)
-    if (ct < 8 * nt * nr) {
-        const uint32_t o = ct >> 3, sl = ct & 7u, t = o / nr, rr = o % nr;
+    for (uint32_t c8 = ct; c8 < 8 * nt * nr; c8 += kCons) {   // whole 8-lane groups
+        const uint32_t o = c8 >> 3, sl = c8 & 7u, t = o / nr, rr = o % nr;
         float s = 0.f;
         for (uint32_t u = sl; u < nu; u += 8)
             if (uniq || ((P->sel[u] >> t) & 1u)) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
         s = rsum<8>(s);
-        if (sl == 7u) a.y[(size_t)t * a.n_embd + r0 + rr] = yv + s;
+        // outputs past the first kCons / 8 read their old y here
+        const float y0 = c8 == ct ? yv : a.y[(size_t)t * a.n_embd + r0 + rr];
+        if (sl == 7u) a.y[(size_t)t * a.n_embd + r0 + rr] = y0 + s;
     }
     Q4MI_TR(30, 1, ct == 0);
 }
