@@ -270,24 +270,23 @@ def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
     lg = torch.from_numpy(synth.logits(rng, T, E, zipf=True)).cuda()
     i32 = torch.int32
     ids, wts = torch.empty(T, k, dtype=i32, device="cuda"), torch.empty(T, k, device="cuda")
-    a_tok, rsrc = torch.empty(rows, dtype=i32, device="cuda"), torch.empty(rows, dtype=i32,
-                                                                            device="cuda")
+    # packed rows: the routed pack, then the shared expert's rows (every
+    # token, in order), which ride in the routed MMQ launches as expert E
+    a_tok = torch.empty(rows + T, dtype=i32, device="cuda")
+    a_tok[rows:] = torch.arange(T, dtype=i32, device="cuda")
+    rsrc = torch.empty(rows, dtype=i32, device="cuda")
     rw = torch.empty(rows, device="cuda")
     stg, stgn = torch.empty(512, dtype=i32, device="cuda"), torch.empty(1, dtype=i32, device="cuda")
-    ek, bounds = torch.empty(512, dtype=i32, device="cuda"), torch.empty(E + 1, dtype=i32,
-                                                                         device="cuda")
-    xq = torch.empty(int(L.q4_mmq_q8_bytes(rows, H)), dtype=torch.uint8, device="cuda")
-    hq = torch.empty(int(L.q4_mmq_q8_bytes(rows, F)), dtype=torch.uint8, device="cuda")
-    pd = torch.empty(rows, H, device="cuda")
-    sb = torch.tensor([0, T], dtype=i32, device="cuda")
-    iden = torch.arange(T, dtype=i32, device="cuda")
-    ones = torch.ones(T, device="cuda")
+    ek = torch.empty(512, dtype=i32, device="cuda")
+    bounds = torch.empty(E + 2, dtype=i32, device="cuda")
+    bounds[E + 1] = rows + T                      # the pack writes bounds[0..E]
+    xq = torch.empty(int(L.q4_mmq_q8_bytes(T, H)), dtype=torch.uint8, device="cuda")
+    hq = torch.empty(int(L.q4_mmq_q8_bytes(rows + T, F)), dtype=torch.uint8, device="cuda")
+    pd = torch.empty(rows + T, H, device="cuda")
     y = torch.zeros(T, H, device="cuda")
     P = q4mi.ptr
     TY = q4mi.T_IQ3_S
     chk = q4mi.check
-
-    hq_s = torch.empty(int(L.q4_mmq_q8_bytes(T, F)), dtype=torch.uint8, device="cuda")
 
     def layer(c):
         A = arenas[c].data_ptr()
@@ -296,18 +295,14 @@ def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
                           P(bounds), T, k, E, T), "assign")
         # q8(x) once per token; routed rows gather it through a_tok
         chk(L.q4_mmq_quantize(P(x), None, P(xq), TY, H, T), "q8 x")
-        chk(L.q4mi_mmq_gate_up(A, TY, F, H, stride, E, P(xq), T, P(a_tok), P(bounds), rows,
-                               P(hq)), "mmq gate/up")
-        chk(L.q4_mmq_mul_id(A + od, TY, H, F, stride, E, P(hq), P(bounds), 0, rows, P(pd), H),
-            "mmq down")
-        chk(L.q4_hip_expert_reduce(P(y), P(pd), P(rsrc), P(rw), T, k, H), "reduce")
-        # shared expert: every token, weight 1
+        # routed experts + the shared expert (its own weight base S; every
+        # token, weight 1) in one gate/up, one down and one reduce launch
         S = A + E * stride
-        chk(L.q4mi_mmq_gate_up(S, TY, F, H, stride, 1, P(xq), T, None, P(sb), T, P(hq_s)),
-            "mmq gate/up shared")
-        chk(L.q4_mmq_mul_id(S + od, TY, H, F, stride, 1, P(hq_s), P(sb), 0, T, P(pd), H),
-            "mmq down shared")
-        chk(L.q4_hip_expert_reduce(P(y), P(pd), P(iden), P(ones), T, 1, H), "reduce shared")
+        chk(L.q4mi_mmq_gate_up_x(A, S, TY, F, H, stride, E, P(xq), T, P(a_tok), P(bounds),
+                                 rows + T, P(hq)), "mmq gate/up")
+        chk(L.q4mi_mmq_mul_id_x(A + od, S + od, TY, H, F, stride, E, P(hq), P(bounds), rows + T,
+                                P(pd), H), "mmq down")
+        chk(L.q4mi_expert_reduce_x(P(y), P(pd), P(rsrc), P(rw), T, k, H, rows, None), "reduce")
 
     def run_all():
         for c in range(copies):

@@ -177,6 +177,28 @@ bool q4mi_mmq_gate_up(const void *w, uint32_t type, uint64_t n_ff, uint64_t w_co
                       uint64_t xrows, const int32_t *act_row, const int32_t *bounds,
                       uint64_t total_rows, void *hq);
 
+/* q4mi_mmq_gate_up / q4_mmq_mul_id over n_expert routed experts at
+ * w + e*expert_stride_bytes plus one more expert, index n_expert, read from
+ * w_extra; bounds has n_expert + 2 entries.  For a shared expert stored apart
+ * from the routed arena (src/q4_moe.c:97-103 names its own tensors): its rows
+ * (every token, appended after the routed pack) ride in the routed launches.
+ * No reference counterpart. */
+bool q4mi_mmq_gate_up_x(const void *w, const void *w_extra, uint32_t type, uint64_t n_ff,
+                        uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                        const void *xq, uint64_t xrows, const int32_t *act_row,
+                        const int32_t *bounds, uint64_t total_rows, void *hq);
+bool q4mi_mmq_mul_id_x(const void *w, const void *w_extra, uint32_t type, uint64_t w_rows,
+                       uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                       const void *xq, const int32_t *bounds, uint64_t total_rows, float *dst,
+                       uint64_t ld_dst);
+/* q4_hip_expert_reduce plus one extra row per token:
+ * d_y[t] += sum_k rw*pd[rsrc] + xw[t]*pd[x_row0 + t] (d_xw NULL: weight 1;
+ * the reference applies the shared expert's sigmoid gate there,
+ * src/q4_moe.c:306).  No reference counterpart. */
+bool q4mi_expert_reduce_x(float *d_y, const float *d_pd, const int32_t *d_rsrc,
+                          const float *d_rw, uint32_t n_tok, uint32_t topk, uint32_t n_embd,
+                          uint64_t x_row0, const float *d_xw);
+
 #ifdef __cplusplus
 }
 #endif

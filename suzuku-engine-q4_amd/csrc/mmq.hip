@@ -75,14 +75,14 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 // expert are packed into one 64-bit word (16 bits per class, class 3 = the
 // 128-row class in the top field), so a single exclusive scan over the
 // experts gives every class's offsets at once: a wave scan, then one step
-// across the 8 waves.  Field sums stay below 2^16 (at most
+// across the 16 waves.  Field sums stay below 2^16 (at most
 // total_rows/mt + n_exp <= 65535 tiles, checked by the caller).  mt (128,
 // 64 or 32) is the tile height: whole tiles are mt rows (class mt/32 - 1).
-__global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ bounds,
+__global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ bounds,
                                                    uint32_t n_exp, uint32_t mt,
                                                    int2 *__restrict__ tiles,
                                                    uint32_t *__restrict__ count, uint32_t cap) {
-    __shared__ uint64_t wsum[8];
+    __shared__ uint64_t wsum[16];
     const uint32_t e = threadIdx.x, lane = e & 63u, w = e >> 6;
     uint32_t n = 0;
     if (e < n_exp) {
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(512) void mmq_tiles_k(const int32_t *__restrict__ b
     __syncthreads();
     uint64_t before = 0, total = 0;
 #pragma unroll
-    for (uint32_t k = 0; k < 8; k++) {
+    for (uint32_t k = 0; k < 16; k++) {
         const uint64_t v = wsum[k];
         if (k < w) before += v;
         total += v;
@@ -177,6 +177,8 @@ struct MmqLds {
 
 struct MmqArgs {
     const uint8_t *w;
+    const uint8_t *wx;      // optional: base of expert ex (else w + ex * estride)
+    uint32_t ex;
     uint64_t estride;       // bytes between experts
     uint32_t rb;            // bytes per weight row
     uint32_t K;             // w_cols
@@ -303,7 +305,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     const uint32_t e = (uint32_t)tinfo.x;
     const int32_t rbase = a.bounds[e] + tinfo.y;
     const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), 32u * NSUB);
-    const uint8_t *We = a.w + (uint64_t)e * a.estride;
+    const uint8_t *We = (a.wx && e == a.ex) ? a.wx : a.w + (uint64_t)e * a.estride;
     // weight row (within the expert) of tile row r
     const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
     auto wrow = [&](uint32_t r) -> uint32_t {
@@ -646,9 +648,13 @@ static bool mmq_launch(const MmqArgs &a, dim3 grid) {
 // its activation row.  Plain mode writes dst[p][0..w_rows); fused mode
 // (w_rows = 2*n_ff, gate rows then up rows) writes the q8 codes of
 // h = silu(gate)*up into hq (the q4_mmq_q8_bytes(total_rows, n_ff) layout).
+// wx (optional) is the base of the last expert, n_exp - 1, which then need
+// not sit at w + (n_exp - 1) * estride (a shared expert kept apart from the
+// routed arena).
 bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, uint64_t estride,
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
-             const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq) {
+             const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq,
+             const uint8_t *wx = nullptr) {
     if (!total_rows) return true;
     // tile height: the largest of 128, 64, 32 rows whose block count (from
     // the whole-tile lower bound) still fills two blocks per CU.  Small
@@ -666,10 +672,12 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
         set_error("mmq: tile buffer allocation failed");
         return false;
     }
-    mmq_tiles_k<<<1, 512, 0, stream()>>>(bounds, n_exp, mt, g_tiles, g_ntiles, max_tiles);
+    mmq_tiles_k<<<1, 1024, 0, stream()>>>(bounds, n_exp, mt, g_tiles, g_ntiles, max_tiles);
     if (!launch_ok("mmq_tiles_k")) return false;
     MmqArgs a;
     a.w = w;
+    a.wx = wx;
+    a.ex = n_exp - 1;
     a.estride = estride;
     a.rb = (uint32_t)q4mi_row_bytes(ty, w_cols);
     a.K = (uint32_t)w_cols;
@@ -817,6 +825,47 @@ bool q4mi_mmq_gate_up(const void *w, uint32_t type, uint64_t n_ff, uint64_t w_co
     }
     return mmq_run((const uint8_t *)w, type, 2 * n_ff, w_cols, expert_stride_bytes, n_expert,
                    xq, xrows, act_row, bounds, total_rows, nullptr, 0, hq);
+}
+
+/* q4mi_mmq_gate_up / q4_mmq_mul_id over n_expert routed experts at
+ * w + e*stride plus one more expert, index n_expert, whose matrix sits at
+ * w_extra (a shared expert stored apart from the routed arena).  bounds has
+ * n_expert + 2 entries.  One launch covers both, so a shared expert over
+ * every token rides in the routed launch instead of its own. */
+bool q4mi_mmq_gate_up_x(const void *w, const void *w_extra, uint32_t type, uint64_t n_ff,
+                        uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                        const void *xq, uint64_t xrows, const int32_t *act_row,
+                        const int32_t *bounds, uint64_t total_rows, void *hq) {
+    if (!w || !w_extra || !xq || !bounds || !hq || !n_expert || n_expert > 1023 || !w_cols ||
+        !xrows || ((uintptr_t)hq & 15) || ((uintptr_t)xq & 15) || n_ff % 64) {
+        set_error("q4mi_mmq_gate_up_x: bad arguments");
+        return false;
+    }
+    if (!mmq_supported(type, 2 * n_ff, w_cols)) {
+        set_error("q4mi_mmq_gate_up_x: type/shape not covered");
+        return false;
+    }
+    return mmq_run((const uint8_t *)w, type, 2 * n_ff, w_cols, expert_stride_bytes, n_expert + 1,
+                   xq, xrows, act_row, bounds, total_rows, nullptr, 0, hq,
+                   (const uint8_t *)w_extra);
+}
+
+bool q4mi_mmq_mul_id_x(const void *w, const void *w_extra, uint32_t type, uint64_t w_rows,
+                       uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                       const void *xq, const int32_t *bounds, uint64_t total_rows, float *dst,
+                       uint64_t ld_dst) {
+    if (!w || !w_extra || !xq || !bounds || !dst || !n_expert || n_expert > 1023 || !w_cols ||
+        !ld_dst || ld_dst % 4 || ((uintptr_t)dst & 15) || ((uintptr_t)xq & 15)) {
+        set_error("q4mi_mmq_mul_id_x: bad arguments");
+        return false;
+    }
+    if (!mmq_supported(type, w_rows, w_cols)) {
+        set_error("q4mi_mmq_mul_id_x: type/shape not covered");
+        return false;
+    }
+    return mmq_run((const uint8_t *)w, type, w_rows, w_cols, expert_stride_bytes, n_expert + 1, xq,
+                   total_rows, nullptr, bounds, total_rows, dst, ld_dst, nullptr,
+                   (const uint8_t *)w_extra);
 }
 
 /* h[r][k] = silu(gu[r][k]) * gu[r][n_ff + k]. */

@@ -217,7 +217,8 @@ __global__ __launch_bounds__(256) void reduce_k(float *__restrict__ dy,
                                                 const float *__restrict__ pd,
                                                 const int32_t *__restrict__ rsrc,
                                                 const float *__restrict__ rw, uint32_t topk,
-                                                uint32_t n_embd) {
+                                                uint32_t n_embd, int64_t x_row0,
+                                                const float *__restrict__ xw) {
     const uint32_t t = blockIdx.y;
     const uint32_t i = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n_embd) return;
@@ -227,6 +228,14 @@ __global__ __launch_bounds__(256) void reduce_k(float *__restrict__ dy,
         if (src < 0) continue;
         const float w = rw[(size_t)t * topk + k];
         const float4 v = *(const float4 *)(pd + (size_t)src * n_embd + i);
+        acc.x += w * v.x;
+        acc.y += w * v.y;
+        acc.z += w * v.z;
+        acc.w += w * v.w;
+    }
+    if (x_row0 >= 0) {   // one more expert row per token: pd[x_row0 + t], weight xw[t] or 1
+        const float w = xw ? xw[t] : 1.f;
+        const float4 v = *(const float4 *)(pd + (size_t)(x_row0 + t) * n_embd + i);
         acc.x += w * v.x;
         acc.y += w * v.y;
         acc.z += w * v.z;
@@ -279,9 +288,10 @@ bool assign_launch(const int32_t *ids, const float *wts, int32_t *a_tok, int32_t
 }
 
 bool reduce_launch(float *dy, const float *pd, const int32_t *rsrc, const float *rw,
-                   uint32_t n_tok, uint32_t topk, uint32_t n_embd) {
+                   uint32_t n_tok, uint32_t topk, uint32_t n_embd, int64_t x_row0 = -1,
+                   const float *xw = nullptr) {
     const dim3 grid((n_embd / 4 + 255) / 256, n_tok);
-    reduce_k<<<grid, dim3(256), 0, stream()>>>(dy, pd, rsrc, rw, topk, n_embd);
+    reduce_k<<<grid, dim3(256), 0, stream()>>>(dy, pd, rsrc, rw, topk, n_embd, x_row0, xw);
     return launch_ok("reduce_k");
 }
 
@@ -363,6 +373,21 @@ bool q4_hip_expert_reduce(float *d_y, const float *d_pd, const int32_t *d_rsrc,
         return false;
     }
     return reduce_launch(d_y, d_pd, d_rsrc, d_rw, n_tok, topk, n_embd);
+}
+
+/* q4_hip_expert_reduce plus one more expert row per token:
+ * dy[t] += sum_k rw * pd[rsrc] + xw[t] * pd[x_row0 + t] (xw NULL: weight 1).
+ * The extra rows are a shared expert's outputs appended after the routed
+ * rows (the _x MMQ entry points). */
+bool q4mi_expert_reduce_x(float *d_y, const float *d_pd, const int32_t *d_rsrc,
+                          const float *d_rw, uint32_t n_tok, uint32_t topk, uint32_t n_embd,
+                          uint64_t x_row0, const float *d_xw) {
+    if (!d_y || !d_pd || !d_rsrc || !d_rw || !n_tok || !topk || (n_embd % 4) ||
+        ((uintptr_t)d_y & 15) || ((uintptr_t)d_pd & 15) || x_row0 > (1ull << 40)) {
+        set_error("q4mi_expert_reduce_x: bad arguments");
+        return false;
+    }
+    return reduce_launch(d_y, d_pd, d_rsrc, d_rw, n_tok, topk, n_embd, (int64_t)x_row0, d_xw);
 }
 
 }  // extern "C"

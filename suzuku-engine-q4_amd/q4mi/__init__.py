@@ -69,6 +69,11 @@ _SIGS = {
                                   _vp, _u64]),
     "q4mi_mmq_gate_up": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp, _u64,
                               _vp]),
+    "q4mi_mmq_gate_up_x": (_b, [_vp, _vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp,
+                                _u64, _vp]),
+    "q4mi_mmq_mul_id_x": (_b, [_vp, _vp, _u32, _u64, _u64, _u64, _u32, _vp, _vp, _u64, _vp,
+                               _u64]),
+    "q4mi_expert_reduce_x": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u64, _vp]),
 }
 
 _lib = None

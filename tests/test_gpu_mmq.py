@@ -243,3 +243,71 @@ def test_gate_up_fused_and_rows(gpu, oracle):
         for r in range(0, len(toks), 17):
             q, d, _ = oracle.quant8(hg[r].astype(np.float32))
             assert np.abs(q.astype(np.float32) - codes[bounds[e] + r]).max() <= 1
+
+
+def test_shared_expert_in_routed_launch(gpu):
+    """The _x entry points (routed experts + a shared expert stored apart,
+    appended as expert E over every token) give the separate launches'
+    results: q8(h) codes bit-exact, y within fp32 reduction order."""
+    import torch
+    E, H, F, T, k = 64, 2048, 512, 512, 4
+    rng = np.random.default_rng(41)
+    arena = synth.expert_arena(rng, E + 1, H, F)
+    stride, og, ou, od = synth.expert_stride(H, F)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    lg = synth.logits(rng, T, E, zipf=True)
+    sw = rng.uniform(0.1, 1.0, T).astype(np.float32)          # per-token shared-expert gate
+    L, P, chk = gpu, q4mi.ptr, q4mi.check
+    d_routed = dev(arena[:E * stride])
+    d_shared = dev(arena[E * stride:(E + 1) * stride].copy())  # its own allocation
+    dx, dlg, dsw = dev(x), dev(lg), dev(sw)
+    ids, wts = zeros((T, k), torch.int32), zeros((T, k))
+    chk(L.q4_hip_route_pf(P(dlg), P(ids), P(wts), T, E, k), "route")
+    rows = T * k
+    a_tok = zeros(rows + T, torch.int32)
+    a_tok[rows:] = torch.arange(T, dtype=torch.int32, device="cuda")
+    rsrc, rw = zeros(rows, torch.int32), zeros(rows)
+    stg, stgn, ek = zeros(512, torch.int32), zeros(1, torch.int32), zeros(512, torch.int32)
+    bounds = zeros(E + 2, torch.int32)
+    bounds[E + 1] = rows + T
+    chk(L.q4mi_assign(P(ids), P(wts), P(a_tok), P(rsrc), P(rw), P(stg), P(stgn), P(ek),
+                      P(bounds), T, k, E, T), "assign")
+    xq = mmq_quant(L, dx, None, H, T)
+    # separate launches
+    hq = zeros(int(L.q4_mmq_q8_bytes(rows, F)), torch.uint8)
+    chk(L.q4mi_mmq_gate_up(P(d_routed), T_IQ3_S, F, H, stride, E, P(xq), T, P(a_tok), P(bounds),
+                           rows, P(hq)), "gate_up")
+    pd = zeros((rows, H))
+    chk(L.q4_mmq_mul_id(P(d_routed) + od, T_IQ3_S, H, F, stride, E, P(hq), P(bounds), 0, rows,
+                        P(pd), H), "down")
+    y1 = zeros((T, H))
+    chk(L.q4_hip_expert_reduce(P(y1), P(pd), P(rsrc), P(rw), T, k, H), "reduce")
+    sb = dev(np.array([0, T], np.int32))
+    hq_s = zeros(int(L.q4_mmq_q8_bytes(T, F)), torch.uint8)
+    chk(L.q4mi_mmq_gate_up(P(d_shared), T_IQ3_S, F, H, stride, 1, P(xq), T, None, P(sb), T,
+                           P(hq_s)), "gate_up shared")
+    pd_s = zeros((T, H))
+    chk(L.q4_mmq_mul_id(P(d_shared) + od, T_IQ3_S, H, F, stride, 1, P(hq_s), P(sb), 0, T,
+                        P(pd_s), H), "down shared")
+    chk(L.q4_hip_expert_reduce(P(y1), P(pd_s), P(dev(np.arange(T, dtype=np.int32))), P(dsw), T,
+                               1, H), "reduce shared")
+    # one launch each
+    hq_x = zeros(int(L.q4_mmq_q8_bytes(rows + T, F)), torch.uint8)
+    chk(L.q4mi_mmq_gate_up_x(P(d_routed), P(d_shared), T_IQ3_S, F, H, stride, E, P(xq), T,
+                             P(a_tok), P(bounds), rows + T, P(hq_x)), "gate_up_x")
+    pd_x = zeros((rows + T, H))
+    chk(L.q4mi_mmq_mul_id_x(P(d_routed) + od, P(d_shared) + od, T_IQ3_S, H, F, stride, E,
+                            P(hq_x), P(bounds), rows + T, P(pd_x), H), "down_x")
+    y2 = zeros((T, H))
+    chk(L.q4mi_expert_reduce_x(P(y2), P(pd_x), P(rsrc), P(rw), T, k, H, rows, P(dsw)), "reduce_x")
+    # the q8(h) layout: fp16 codes [rows][F] then fp32 scales [rows][F/32]
+    def codes(buf, n):
+        b = host(buf)
+        return (b[:n * F * 2].view(np.float16), b[n * F * 2:n * F * 2 + n * F // 32 * 4].view(np.float32))
+    cx, dxs = codes(hq_x, rows + T)
+    cr, dr = codes(hq, rows)
+    cs, ds = codes(hq_s, T)
+    assert np.array_equal(cx[:rows * F], cr) and np.array_equal(dxs[:rows * F // 32], dr)
+    assert np.array_equal(cx[rows * F:], cs) and np.array_equal(dxs[rows * F // 32:], ds)
+    assert np.array_equal(host(pd_x)[:rows], host(pd)) and np.array_equal(host(pd_x)[rows:], host(pd_s))
+    assert rel_err(host(y2), host(y1)) <= 1e-5
