@@ -101,13 +101,29 @@ __device__ inline void row_dot(const Iq3sLds *tab, const uint8_t *lb, const uint
 
 // Copy nbytes (even) from global src to LDS dst with the widest aligned
 // accesses the addresses allow; all threads of the block take part.
+// One 16-byte-per-lane global -> LDS copy of the calling wave (gfx950
+// global_load_lds_dwordx4): lane i's 16 bytes at g land at LDS byte address
+// lds + 16 i.  Inline asm, so the compiler adds no waits of its own.
+__device__ inline void lds_dma16(const void *g, uint32_t lds) {
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(lds) : "memory", "m0");
+}
+
 __device__ inline void stage_tile(uint8_t *dst, const uint8_t *src, uint32_t nbytes,
                                   uint32_t tid, uint32_t nthr) {
     const uintptr_t a = (uintptr_t)src | nbytes;
     if ((a & 15u) == 0) {
-        const uint4 *s = (const uint4 *)src;
-        uint4 *d = (uint4 *)dst;
-        for (uint32_t i = tid; i < nbytes / 16; i += nthr) d[i] = s[i];
+        // every copy of the block in flight at once (1 KB per wave op), one
+        // wait; the caller's barrier makes the other waves' parts visible
+        const uint32_t lane = tid & 63u, nw = nthr / 64;
+        const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t l0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+        for (uint32_t j = w; j < (nbytes + 1023) / 1024; j += nw) {
+            const uint32_t off = 1024u * j + 16u * lane;
+            if (off < nbytes) lds_dma16(src + off, l0 + 1024u * j);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else if ((a & 3u) == 0) {
         const uint32_t *s = (const uint32_t *)src;
         uint32_t *d = (uint32_t *)dst;
