@@ -76,6 +76,9 @@ void q4_hip_moe_scratch_warm(void);
 /* Measurement hook: 1 = gate/up launch only, 2 = down only, 3 = both
  * (default).  No reference counterpart. */
 void q4mi_moe_phases(int mask);
+/* Test hook: cap the decode kernels' LDS at `bytes` (0: all of it), so their
+ * LDS rings get reused within a launch.  No reference counterpart. */
+void q4mi_moe_lds_cap(uint32_t bytes);
 /* One token; slots/wts are HOST arrays of n <= 64 experts.
  * d_y[r] += sum_e wts[e] * down_e(q8(silu(gate_e.q8(x)) * up_e.q8(x))).
  * gt == ut; IQ3_S or Q8_0; in_dim == n_embd.  d_h, d_h2, d_down are

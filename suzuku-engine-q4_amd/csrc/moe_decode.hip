@@ -53,7 +53,6 @@ constexpr uint32_t kCons = kT - kProd * 64;   // consumer threads
 constexpr uint32_t kConsW = kCons / 64;       // consumer waves
 constexpr uint32_t kDnRows = 8;   // output rows per down block
 constexpr uint32_t kMaxS = 16;    // LDS ring slots
-
 struct HostList {
     int32_t id[kMaxU];
     float w[kMaxU];
@@ -380,10 +379,10 @@ struct MoeArgs {
 // Optional build (-DQ4MI_TRACE): the first producer and the first consumer
 // thread of every block record wall-clock phase timestamps (10 ns ticks).
 #ifdef Q4MI_TRACE
-#define Q4MI_TR_DECL unsigned long long *const q4tr = a.trace
-#define Q4MI_TR(k, kern, who) do { if (q4tr && (who)) q4tr[((size_t)(kern) * 4096 + blockIdx.x) * 32 + (k)] = wall_clock64(); } while (0)
+#define Q4MI_TR_DECL(b) unsigned long long *const q4tr = a.trace; const uint32_t q4bid = (b)
+#define Q4MI_TR(k, kern, who) do { if (q4tr && (who)) q4tr[((size_t)(kern) * 4096 + q4bid) * 32 + (k)] = wall_clock64(); } while (0)
 #else
-#define Q4MI_TR_DECL do { } while (0)
+#define Q4MI_TR_DECL(b) do { } while (0)
 #define Q4MI_TR(k, kern, who) do { } while (0)
 #endif
 
@@ -447,6 +446,7 @@ __device__ inline float silu_f(float v) { return v / (1.f + expf(-v)); }
 //   Sync::landed[p]  chunks of producer p that have landed (chunk c belongs
 //                    to producer c % kProd, landed in order)
 //   Sync::cons[s]    items finished in the chunk held by ring slot s
+//   Sync::owner[s]   that chunk's index
 //   Sync::ready      consumer waves done with the shared prologue work
 //   Sync::fin        consumer waves done with every item
 struct Sync {
@@ -454,6 +454,7 @@ struct Sync {
     uint32_t fin;
     uint32_t landed[kProd];
     uint32_t cons[kMaxS];
+    uint32_t owner[kMaxS];   // chunk last issued into ring slot s
 };
 
 __device__ inline uint32_t lds_ld(const uint32_t *p) { return *(const volatile uint32_t *)p; }
@@ -484,13 +485,19 @@ template <class IssueFn, class ItemsFn, class TraceFn>
 __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, uint32_t S,
                                uint32_t &issued, IssueFn issue, ItemsFn items, TraceFn trace) {
     uint32_t next = p, pub = p;    // next chunk to issue / to publish
+    // Slot c % S is free for chunk c once chunk c - S (its previous user,
+    // possibly another producer's) was issued there and fully consumed.  The
+    // owner check matters when S is not a multiple of kProd: the count alone
+    // could still be the one left by chunk c - 2S.
     auto slot_free = [&](uint32_t c) {
-        return c < S || lds_ld(&y->cons[c % S]) >= items(c - S);
+        return c < S || (lds_ld(&y->owner[c % S]) == c - S &&
+                         lds_ld(&y->cons[c % S]) >= items(c - S));
     };
     uint32_t idle = 0;
     while (pub < C && idle < kSpinMax) {
         while (next < C && (next < pub + kProd * kMaxS) && slot_free(next)) {
             if (next >= S) lds_st(&y->cons[next % S], 0);
+            lds_st(&y->owner[next % S], next);
             issue(next);
             ends[(next / kProd) % kMaxS] = issued;
             next += kProd;
@@ -517,10 +524,13 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
 //
 // LDS: [stab 32 KB] (IQ3_S) Plan Sync | xq [NT][K] | xd [NT][K/32] | ring of
 //      S slots, slot = gate rows[ch] then up rows[ch].
+//
+// Block `bid` of `nblk` takes pairs [PT*bid/nblk, PT*(bid+1)/nblk).
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Q4MI_TR_DECL;
+__device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, uint8_t *smem,
+                                                              uint32_t bid, uint32_t nblk,
+                                                              uint32_t ch, uint32_t S) {
+    Q4MI_TR_DECL(bid);
     Q4MI_TR(31, 0, threadIdx.x == 0);
     constexpr bool kIq = TY == Q4MI_T_IQ3_S;
     uint32_t *stab = (uint32_t *)smem;
@@ -532,7 +542,6 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nt = a.src.n_tok, K = a.K, n_ff = a.n_ff, rb = a.rb_gu;
-    const uint32_t ch = a.chunk, S = a.slots;
     const uint32_t slot_bytes = 2u * ch * rb;
     const KArgs ka = kargs();
     const bool uniq = a.src.unique != 0;
@@ -554,8 +563,8 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
     const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
     const uint32_t PT = nu * n_ff;
-    const uint32_t p0 = (uint32_t)(((uint64_t)PT * blockIdx.x) / gridDim.x);
-    const uint32_t p1 = (uint32_t)(((uint64_t)PT * (blockIdx.x + 1)) / gridDim.x);
+    const uint32_t p0 = (uint32_t)(((uint64_t)PT * bid) / nblk);
+    const uint32_t p1 = (uint32_t)(((uint64_t)PT * (bid + 1)) / nblk);
     const uint32_t np = p1 - p0;
     const uint32_t C = (np + ch - 1) / ch;
 
@@ -650,6 +659,12 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     Q4MI_TR(30, 0, ct == 0);
 }
 
+template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
+__global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    gu_body<TY, NT, TPR, GPT, UNIT>(a, smem, blockIdx.x, gridDim.x, a.chunk, a.slots);
+}
+
 // ---------------------------------------------------------------- down
 // Same roles.  Items are (expert u, output row rr); the chunks are runs of
 // `ch` experts (kDnRows rows each).  The consumers quantize every selected
@@ -658,10 +673,13 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
 // LDS: [stab] Plan Sync | part [kMaxU][NT][kDnRows] | hq [nsel_cap][n_ff] |
 //      hd [nsel_cap][n_ff/32] | ring of S slots, slot = ch experts x kDnRows
 //      rows.
+//
+// Block `bid` owns output rows 8*bid..
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Q4MI_TR_DECL;
+__device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, uint8_t *smem,
+                                                              uint32_t bid, uint32_t ch,
+                                                              uint32_t S) {
+    Q4MI_TR_DECL(bid);
     Q4MI_TR(31, 1, threadIdx.x == 0);
     constexpr bool kIq = TY == Q4MI_T_IQ3_S;
     uint32_t *stab = (uint32_t *)smem;
@@ -675,8 +693,7 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nt = a.src.n_tok, rb = a.rb_dn;
-    const uint32_t ch = a.chunk, S = a.slots;
-    const uint32_t r0 = blockIdx.x * kDnRows;
+    const uint32_t r0 = bid * kDnRows;
     const uint32_t nr = min(kDnRows, a.n_embd - r0);
     const uint32_t slot_bytes = ch * kDnRows * rb;
     const KArgs ka = kargs();
@@ -841,40 +858,83 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     Q4MI_TR(30, 1, ct == 0);
 }
 
+template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
+__global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    dn_body<TY, NT, TPR, GPT, UNIT>(a, smem, blockIdx.x, a.chunk, a.slots);
+}
+
 // ------------------------------------------------------------------ host
 constexpr size_t kLdsCap = 160 * 1024;
+
+// LDS budget of a decode block (q4mi_moe_lds_cap lowers it for tests).
+static size_t g_lds_cap = 0;
+static size_t lds_cap() { return g_lds_cap ? std::min(g_lds_cap, kLdsCap) : kLdsCap; }
 
 static size_t head_bytes(uint32_t ty) {
     return al16((ty == Q4MI_T_IQ3_S ? 32768 : 0) + sizeof(Plan) + sizeof(Sync));
 }
 
-template <uint32_t TY, int NT, int TPR, int GPT>
-static bool launch_gu(MoeArgs a, uint32_t nu_host) {
-    const uint32_t grid = (uint32_t)cu_count();
+// Chunk size and ring slots of the gate/up kernel for `grid` blocks within
+// `cap` bytes of LDS; returns the LDS bytes (0: does not fit).
+template <int NT>
+static size_t gu_plan(const MoeArgs &a, uint32_t nu_host, uint32_t grid, size_t cap,
+                      uint32_t &ch, uint32_t &S, uint32_t ty) {
     // one chunk per producer wave when it fits (a producer publishes a chunk
     // only after issuing everything before it, so a second chunk would
     // delay the first); device lists (unknown share) use 8 pairs
     const uint32_t pairs = nu_host ? nu_host * a.n_ff : kMaxU * a.n_ff;
     const uint32_t share = (pairs + grid - 1) / grid;
-    uint32_t ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : 8;
-    const size_t fixed = head_bytes(TY) + al16((size_t)NT * a.K + (size_t)NT * (a.K / 32) * 4);
-    uint32_t S = 0;
+    ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : 8;
+    const size_t fixed = head_bytes(ty) + al16((size_t)NT * a.K + (size_t)NT * (a.K / 32) * 4);
+    S = 0;
     // A consumer wave waits for every chunk its two pairs touch (at most
     // two), so a reused ring needs three slots to always make progress.
     for (;; ch = (ch + 1) / 2) {
         const size_t slot = 2ull * ch * a.rb_gu;
-        S = fixed < kLdsCap ? (uint32_t)std::min<size_t>(kMaxS, (kLdsCap - fixed) / slot) : 0;
+        S = fixed < cap ? (uint32_t)std::min<size_t>(kMaxS, (cap - fixed) / slot) : 0;
         if (S >= 3 || ch == 1) break;
     }
     const uint32_t C = (share + ch - 1) / ch;
-    if (S < 3 && S < C) {
+    if (S < 3 && S < C) return 0;
+    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
+    return fixed + (size_t)S * 2 * ch * a.rb_gu;
+}
+
+// Same for the down kernel (sets a.nsel_cap).
+template <int NT>
+static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &ch, uint32_t &S,
+                      uint32_t ty) {
+    const uint32_t cap = nu_host ? nu_host : kMaxU;   // selected pairs (<= 64)
+    const size_t fixed = head_bytes(ty) + (size_t)kMaxU * NT * kDnRows * 4 +
+                         al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
+    const uint32_t nu_est = nu_host ? nu_host : kMaxU;
+    ch = std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd);
+    S = 0;
+    for (;; ch = (ch + 1) / 2) {
+        const size_t slot = (size_t)ch * kDnRows * a.rb_dn;
+        S = fixed < cap_bytes ? (uint32_t)std::min<size_t>(kMaxS, (cap_bytes - fixed) / slot) : 0;
+        if (S >= 2 || ch == 1) break;
+    }
+    // a consumer wave's 64/TPR (<= 8) consecutive items touch at most two chunks (ch * kDnRows >= 8)
+    const uint32_t C = (nu_est + ch - 1) / ch;
+    if (S < 2 && S < C) return 0;
+    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
+    a.nsel_cap = cap;
+    return fixed + (size_t)S * ch * kDnRows * a.rb_dn;
+}
+
+template <uint32_t TY, int NT, int TPR, int GPT>
+static bool launch_gu(MoeArgs a, uint32_t nu_host) {
+    const uint32_t grid = (uint32_t)cu_count();
+    uint32_t ch, S;
+    const size_t lds = gu_plan<NT>(a, nu_host, grid, lds_cap(), ch, S, TY);
+    if (!lds) {
         set_error("moe_gu_k: LDS limit");
         return false;
     }
-    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
     a.chunk = ch;
     a.slots = S;
-    const size_t lds = fixed + (size_t)S * 2 * ch * a.rb_gu;
     const bool wide = ((((uintptr_t)a.base) | a.stride | a.og | a.ou | a.rb_gu) & 15u) == 0;
     const void *fn = wide ? (const void *)moe_gu_k<TY, NT, TPR, GPT, 16>
                           : (const void *)moe_gu_k<TY, NT, TPR, GPT, 4>;
@@ -891,28 +951,14 @@ static bool launch_gu(MoeArgs a, uint32_t nu_host) {
 
 template <uint32_t TY, int NT, int TPR, int GPT>
 static bool launch_dn(MoeArgs a, uint32_t nu_host) {
-    const uint32_t cap = nu_host ? nu_host : kMaxU;   // selected pairs (<= 64)
-    const size_t fixed = head_bytes(TY) + (size_t)kMaxU * NT * kDnRows * 4 +
-                         al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
-    const uint32_t nu_est = nu_host ? nu_host : kMaxU;
-    uint32_t ch = std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd);
-    uint32_t S = 0;
-    for (;; ch = (ch + 1) / 2) {
-        const size_t slot = (size_t)ch * kDnRows * a.rb_dn;
-        S = fixed < kLdsCap ? (uint32_t)std::min<size_t>(kMaxS, (kLdsCap - fixed) / slot) : 0;
-        if (S >= 2 || ch == 1) break;
-    }
-    // a consumer wave's 64/TPR (<= 8) consecutive items touch at most two chunks (ch * kDnRows >= 8)
-    const uint32_t C = (nu_est + ch - 1) / ch;
-    if (S < 2 && S < C) {
+    uint32_t ch, S;
+    const size_t lds = dn_plan<NT>(a, nu_host, lds_cap(), ch, S, TY);
+    if (!lds) {
         set_error("moe_dn_k: LDS limit");
         return false;
     }
-    S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
     a.chunk = ch;
     a.slots = S;
-    a.nsel_cap = cap;
-    const size_t lds = fixed + (size_t)S * ch * kDnRows * a.rb_dn;
     // a block copies one contiguous run of kDnRows rows per expert: 16-byte
     // units need that run (not each row) 16-byte aligned and sized
     const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | ((uint64_t)kDnRows * a.rb_dn)) & 15u) == 0 &&
@@ -1080,6 +1126,10 @@ extern "C" {
 
 /* Benchmark hook: 1 = gate/up launch only, 2 = down only, 3 = both. */
 void q4mi_moe_phases(int mask) { g_phases = mask & 3; }
+
+/* Test hook: cap the decode kernels' LDS at `bytes` (0: the CU's 160 KB), so
+ * that their LDS rings are reused within a launch. */
+void q4mi_moe_lds_cap(uint32_t bytes) { g_lds_cap = bytes; }
 
 /* Allocate the decode scratch (call before any stream capture). */
 void q4_hip_moe_scratch_warm(void) {

@@ -45,6 +45,7 @@ _SIGS = {
     "q4mi_mmvq": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _u32, _vp, _f32, _vp]),
     "q4_hip_moe_scratch_warm": (None, []),
     "q4mi_moe_phases": (None, [_c.c_int]),
+    "q4mi_moe_lds_cap": (None, [_u32]),
     "q4_hip_moe_exec": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32, _u64,
                              _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_exec_dev": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u64, _u32, _u64, _u32, _u64,

@@ -43,6 +43,13 @@ def gpu():
     return L
 
 
+def layer_err(got, ref):
+    """max |got-ref| / max|ref| (normwise)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
 def rel_err(got, ref):
     """max |got-ref| / max(|ref|, 1e-3 * max|ref|): elementwise relative error
     with values near zero measured against 1e-3 of the output's scale."""
