@@ -115,6 +115,20 @@ def test_mmvq_batch_invariant(gpu):
         assert np.array_equal(yn.view(np.uint32), y8[:nt].view(np.uint32))
 
 
+@pytest.mark.parametrize("ty,rows,nt", [(T_Q8_0, 20003, 1), (T_Q8_0, 20003, 4),
+                                          (T_IQ3_S, 33003, 1), (T_IQ3_S, 33003, 4)])
+def test_mmvq_large(gpu, oracle, ty, rows, nt):
+    """Tall matrices (thousands of row tiles, lm_head-like); the last tile is
+    ragged."""
+    rng = np.random.default_rng(rows + nt)
+    K = 2048
+    w = synth.matrix(rng, ty, rows, K)
+    x = rng.standard_normal((nt, K)).astype(np.float32)
+    y, _ = mmvq_gpu(gpu, ty, w, rows, K, x)
+    yo = oracle.dot8_rows(ty, w, rows, K, x)
+    assert rel_err(y, yo) <= TOL
+
+
 def test_q4_mmvq_n_abi(gpu, oracle):
     """The reference's q4_mmvq_n entry: fp32 x in, y[t*rows+r] = scale*dot."""
     import torch
