@@ -20,6 +20,18 @@ __device__ inline uint32_t f2key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Wave maximum of an unsigned value (DPP row shifts, then the row
+// broadcasts; the total lands in lane 63), returned to every lane.
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, true));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // One wave per token; up to 512 experts (8 per lane), k <= 64.
 // Ranking uses (logit desc, index asc): softmax is monotonic, so this is the
 // host's (probability desc, index asc) order except where two different
@@ -60,21 +72,20 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
         if ((lane + 64u * j) < n_exp) alive |= 1u << j;
     const uint32_t tk = topk < n_exp ? topk : n_exp;
     for (uint32_t k = 0; k < tk; k++) {
-        uint64_t best = 0;
+        // this lane's best alive entry: largest key, smallest index on ties
+        uint32_t bk = 0, bj = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t i = lane + 64u * j;
-            if (alive & (1u << j)) {
-                const uint64_t key = ((uint64_t)f2key(v[j]) << 32) | (uint32_t)(~i);
-                best = key > best ? key : best;
+            const uint32_t key = (alive & (1u << j)) ? f2key(v[j]) : 0u;
+            if (key > bk) {
+                bk = key;
+                bj = (uint32_t)j;
             }
         }
-#pragma unroll
-        for (int o = 32; o; o >>= 1) {
-            const uint64_t b2 = __shfl_xor(best, o);
-            best = b2 > best ? b2 : best;
-        }
-        const uint32_t wi = ~(uint32_t)(best & 0xffffffffu);
+        // wave max of the keys, then the smallest index holding it (two DPP
+        // reductions; the min runs as a max of complements)
+        const uint32_t m = wave_max_u32(bk);
+        const uint32_t wi = ~wave_max_u32(bk == m && bk ? ~(lane + 64u * bj) : 0u);
         if ((wi & 63u) == lane) {
             const uint32_t j = wi >> 6;
             alive &= ~(1u << j);
@@ -160,10 +171,15 @@ __global__ __launch_bounds__(512) void pack_place_k(
     // expert tid: rows in the whole group and in the chunks before this one
     uint32_t tot = 0, before = 0;
     const uint32_t *hg = hist + (size_t)g * nch * 512 + tid;
-    for (uint32_t c2 = 0; c2 < nch; c2++) {
-        const uint32_t v = hg[(size_t)c2 * 512];
-        tot += v;
-        before += c2 < c ? v : 0u;
+    for (uint32_t c0 = 0; c0 < nch; c0 += 8) {   // eight loads in flight at a time
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) v[k] = c0 + k < nch ? hg[(size_t)(c0 + k) * 512] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            tot += v[k];
+            before += c0 + k < c ? v[k] : 0u;
+        }
     }
     for (uint32_t k = tid; k < 8 * 512; k += 512) (&s_wc[0][0])[k] = 0;
     const uint32_t incl = scan512(tot, s_tmp, tid);
