@@ -144,7 +144,6 @@ __global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ 
 constexpr int MMQ_NB = 128;      // weight rows per block
 // token sub-tiles whose MFMA chains are interleaved (two measured no faster
 // than one, and one keeps the register budget clear of spills)
-template <bool FUSED> constexpr int mmq_tp() { return 1; }
 constexpr int MMQ_MB = 128;      // token rows per block
 
 // Raw superblock slots in LDS.  A row's slot holds the dwords covering its
@@ -440,42 +439,48 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         // in memory (the slot begins at the enclosing dword)
         const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);   // same for every row
         const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
+        half8_t A[2][2];
 #pragma unroll
-        for (int gl = 0; gl < 2; gl++) {
-            const uint32_t j = 2 * q + gl;            // group inside the superblock
-            half8_t A0, A1;
-            decode_a<TY>(L, R, j, kh, A0, A1);
+        for (int gl = 0; gl < 2; gl++) decode_a<TY>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
+        // The stage's 2*NSUB products n = (group gl, token sub-tile t): an
+        // exact-integer MFMA pair, then one scale FMA per output.  Product
+        // n+1's pair is issued before product n's FMAs, so the FMAs never
+        // wait on the pair right before them.
+        auto prod = [&](int n, float &dxo) __attribute__((always_inline)) {
+            const int gl = n / NSUB, t = n % NSUB;
             const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
-            constexpr int TP = (NSUB % 2 == 0) ? mmq_tp<FUSED>() : 1;
+            const uint32_t tok = 32 * t + (lane & 31u);
+            const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
+            const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
+            dxo = L.dx[buf][tok][gl];
+            f32x16_t r = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, f32x16_t{}, 0, 0, 0);
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, r, 0, 0, 0);
+        };
+        auto scale = [&](int n, const f32x16_t &sacc, float dxv) __attribute__((always_inline)) {
+            const int gl = n / NSUB, t = n % NSUB;
+            if (TY == Q4MI_T_IQ3_S) {
 #pragma unroll
-            for (int tp = 0; tp < NSUB; tp += TP) {   // TP token sub-tiles at a time
-                f32x16_t sacc[TP];
-                float dxv[TP];
+                for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
+            } else {
+                const uint32_t j = 2 * q + gl;
 #pragma unroll
-                for (int u = 0; u < TP; u++) {
-                    const uint32_t tok = 32 * (tp + u) + (lane & 31u);
-                    const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
-                    const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
-                    sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, f32x16_t{}, 0, 0, 0);
-                    sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, sacc[u], 0, 0, 0);
-                    dxv[u] = L.dx[buf][tok][gl];
-                }
-#pragma unroll
-                for (int u = 0; u < TP; u++) {
-                    const int t = tp + u;
-                    if (TY == Q4MI_T_IQ3_S) {
-#pragma unroll
-                        for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[u][i], dxv[u], inner[t][i]);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 16; i++) {
-                            const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                            const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][roff] + 34 * j));
-                            acc[t][i] = fmaf(sacc[u][i], dxv[u] * dw, acc[t][i]);
-                        }
-                    }
+                for (int i = 0; i < 16; i++) {
+                    const uint32_t nr = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
+                    const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][nr][roff] + 34 * j));
+                    acc[t][i] = fmaf(sacc[i], dxv * dw, acc[t][i]);
                 }
             }
+        };
+        float dcur;
+        f32x16_t cur = prod(0, dcur);
+#pragma unroll
+        for (int n = 0; n < 2 * NSUB; n++) {
+            float dnext = 0.f;
+            f32x16_t nxt{};
+            if (n + 1 < 2 * NSUB) nxt = prod(n + 1, dnext);
+            scale(n, cur, dcur);
+            cur = nxt;
+            dcur = dnext;
         }
         if (TY == Q4MI_T_IQ3_S && q == 3) {   // superblock done: acc += inner * d_w
 #pragma unroll
