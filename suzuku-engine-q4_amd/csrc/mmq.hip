@@ -286,6 +286,9 @@ __device__ inline void mmq_wait(uint32_t n) {
 #undef MMQ_VM_CASE
 // workgroup barrier that leaves this kernel's copies in flight
 __device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// barrier that also leaves this wave's LDS reads in flight (the caller knows
+// none of them reads a buffer another wave refills after it)
+__device__ inline void mmq_bar_rd() { asm volatile("s_barrier" ::: "memory"); }
 
 // One (expert, weight block, token tile) of NSUB 32-row token sub-tiles.
 template <uint32_t TY, bool FUSED, int NSUB>
@@ -420,9 +423,25 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     issue_stage(0);
     for (uint32_t s = 0; s < nst; s++) {
         const uint32_t sbi = s >> 2, q = s & 3u;
+        // the row's raw bytes start at the same offset inside its slot as
+        // in memory (the slot begins at the enclosing dword)
+        const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);   // same for every row
+        // Weight operands of the stage's two groups.  Past stage 0 they are
+        // decoded ahead of the barriers: superblock sbi's raw bytes are in
+        // LDS since stage 4 sbi - 3 (stage 0 waits for them below), and
+        // their buffer is refilled only after the first barrier of stage
+        // 4 sbi + 4.
+        half8_t A[2][2];
+        auto decode = [&]() __attribute__((always_inline)) {
+            const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
+#pragma unroll
+            for (int gl = 0; gl < 2; gl++) decode_a<TY>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
+        };
+        if (s != 0) decode();
         // every wave is done with stage s-1 (and at a superblock start with
-        // superblock sbi-1): their buffers may be refilled
-        mmq_bar();
+        // superblock sbi-1): their buffers may be refilled.  The reads in
+        // flight here are the decode's, of a buffer nobody refills now.
+        mmq_bar_rd();
         uint32_t later = 0;
         if (q == 0 && sbi + 1 < nsb) {
             issue_raw(sbi + 1);
@@ -435,13 +454,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         mmq_wait(later);                              // this wave's part of stage s is in
         mmq_bar();                                    // everyone's part is
         const uint32_t buf = s & 1u;
-        // the row's raw bytes start at the same offset inside its slot as
-        // in memory (the slot begins at the enclosing dword)
-        const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);   // same for every row
-        const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
-        half8_t A[2][2];
-#pragma unroll
-        for (int gl = 0; gl < 2; gl++) decode_a<TY>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
+        if (s == 0) decode();
         // The stage's 2*NSUB products n = (group gl, token sub-tile t): an
         // exact-integer MFMA pair, then one scale FMA per output.  Product
         // n+1's pair is issued before product n's FMAs, so the FMAs never
