@@ -268,9 +268,10 @@ __device__ inline void mmq_copy(const void *g, uint32_t lds_addr) {
         asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                      :: "v"(g), "s"(lds_addr) : "memory", "m0");
 }
-__device__ inline uint32_t mmq_lds(const void *p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
+// LDS address of a generic pointer into LDS: the low half of a flat
+// address in the LDS aperture is the LDS offset (an address-space cast would
+// add a null check to every copy)
+__device__ inline uint32_t mmq_lds(const void *p) { return (uint32_t)(uintptr_t)p; }
 #define MMQ_VM_CASE(n) case n: asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); break;
 // wait until at most n of this wave's copies are in flight (n <= 24 here)
 __device__ inline void mmq_wait(uint32_t n) {
@@ -337,21 +338,19 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     }
     // source rows of this lane's copies: activation op m covers tile rows
     // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
+    // (rows past the tile's end copy the last row's bytes: their outputs are
+    // never stored, and the copy stays one instruction)
     const _Float16 *arow_src[NSUB];
-    bool arow_ok[NSUB];
 #pragma unroll
     for (int m = 0; m < NSUB; m++) {
         const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
-        arow_ok[m] = r < mrows;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
         const int64_t xr = a.act_row ? a.act_row[p] : p;
         arow_src[m] = a.xq + (uint64_t)xr * a.K;
     }
     const float *drow_src;
-    bool drow_ok;
     {
         const uint32_t r = 32 * wv + lane / 2;
-        drow_ok = r < mrows;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
         const int64_t xr = a.act_row ? a.act_row[p] : p;
         drow_src = a.xd + (uint64_t)xr * (a.K / 32);
@@ -367,12 +366,10 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             const uint32_t j = wv + 4 * m;            // 8 rows per op
             const uint32_t r = 8 * j + lane / 8;
             const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
-            // rows past the tile's end copy a valid row's bytes (their
-            // outputs are never stored); one copy instruction either way
-            const _Float16 *src = arow_ok[m] ? arow_src[m] + s * 64 + c * 8 : arow_src[m];
+            const _Float16 *src = arow_src[m] + s * 64 + c * 8;
             mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
         }
-        const float *dsrc = drow_ok ? drow_src + s * 2 + (lane & 1u) : drow_src;
+        const float *dsrc = drow_src + s * 2 + (lane & 1u);
         mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
     };
     // copies of superblock sbi's raw weight bytes into buffer sbi & 1
