@@ -190,7 +190,7 @@ __device__ inline void stage_tile(uint8_t *dst, const uint8_t *src, uint32_t nby
         // wait; the caller's barrier makes the other waves' parts visible
         const uint32_t lane = tid & 63u, nw = nthr / 64;
         const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const uint32_t l0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+        const uint32_t l0 = (uint32_t)(uintptr_t)dst;   // LDS offset: low half of the flat address
         for (uint32_t j = w; j < (nbytes + 1023) / 1024; j += nw) {
             const uint32_t off = 1024u * j + 16u * lane;
             if (off < nbytes) lds_dma16(src + off, l0 + 1024u * j);

@@ -169,9 +169,9 @@ __device__ inline void lds_copy(const void *g, uint32_t lds_addr) {
                      :: "v"(g), "s"(lds_addr) : "memory", "m0");
 }
 
-__device__ inline uint32_t lds_addr_of(const void *p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
+// LDS address of a generic pointer into LDS: the low half of a flat address
+// in the LDS aperture (an address-space cast would add a null check)
+__device__ inline uint32_t lds_addr_of(const void *p) { return (uint32_t)(uintptr_t)p; }
 
 // Asynchronous copy of `bytes` (a multiple of UNIT, both ends UNIT-aligned)
 // global -> LDS by the calling wave, in operations of 64*UNIT bytes.
