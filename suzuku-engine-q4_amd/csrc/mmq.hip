@@ -272,19 +272,12 @@ __device__ inline void mmq_copy(const void *g, uint32_t lds_addr) {
 // address in the LDS aperture is the LDS offset (an address-space cast would
 // add a null check to every copy)
 __device__ inline uint32_t mmq_lds(const void *p) { return (uint32_t)(uintptr_t)p; }
-#define MMQ_VM_CASE(n) case n: asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); break;
-// wait until at most n of this wave's copies are in flight (n <= 24 here)
-__device__ inline void mmq_wait(uint32_t n) {
-    switch (__builtin_amdgcn_readfirstlane(n)) {
-        MMQ_VM_CASE(0) MMQ_VM_CASE(1) MMQ_VM_CASE(2) MMQ_VM_CASE(3) MMQ_VM_CASE(4)
-        MMQ_VM_CASE(5) MMQ_VM_CASE(6) MMQ_VM_CASE(7) MMQ_VM_CASE(8) MMQ_VM_CASE(9)
-        MMQ_VM_CASE(10) MMQ_VM_CASE(11) MMQ_VM_CASE(12) MMQ_VM_CASE(13) MMQ_VM_CASE(14)
-        MMQ_VM_CASE(15) MMQ_VM_CASE(16) MMQ_VM_CASE(17) MMQ_VM_CASE(18) MMQ_VM_CASE(19)
-        MMQ_VM_CASE(20) MMQ_VM_CASE(21) MMQ_VM_CASE(22) MMQ_VM_CASE(23) MMQ_VM_CASE(24)
-        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    }
+// wait until at most N of this wave's copies are in flight
+template <uint32_t N>
+__device__ inline void mmq_wait() {
+    static_assert(N <= 63, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-#undef MMQ_VM_CASE
 // workgroup barrier that leaves this kernel's copies in flight
 __device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // barrier that also leaves this wave's LDS reads in flight (the caller knows
@@ -439,16 +432,15 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         // superblock sbi-1): their buffers may be refilled.  The reads in
         // flight here are the decode's, of a buffer nobody refills now.
         mmq_bar_rd();
-        uint32_t later = 0;
-        if (q == 0 && sbi + 1 < nsb) {
-            issue_raw(sbi + 1);
-            later += RAW_PER_WAVE;
-        }
-        if (s + 1 < nst) {
-            issue_stage(s + 1);
-            later += ST_OPS;
-        }
-        mmq_wait(later);                              // this wave's part of stage s is in
+        // issue the next copies, then wait for this wave's part of stage s
+        // (the copies just issued stay in flight)
+        const bool nraw = q == 0 && sbi + 1 < nsb, nstage = s + 1 < nst;
+        if (nraw) issue_raw(sbi + 1);
+        if (nstage) issue_stage(s + 1);
+        if (nraw && nstage) mmq_wait<RAW_PER_WAVE + ST_OPS>();
+        else if (nstage) mmq_wait<ST_OPS>();
+        else if (nraw) mmq_wait<RAW_PER_WAVE>();
+        else mmq_wait<0>();
         mmq_bar();                                    // everyone's part is
         const uint32_t buf = s & 1u;
         if (s == 0) decode();
