@@ -80,13 +80,15 @@ __global__ __launch_bounds__(256) void mmq_quant_k(const float *__restrict__ x,
 // 64 or 32) is the tile height: whole tiles are mt rows (class mt/32 - 1).
 __global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ bounds,
                                                    uint32_t n_exp, uint32_t mt,
-                                                   int2 *__restrict__ tiles,
+                                                   int4 *__restrict__ tiles,
                                                    uint32_t *__restrict__ count, uint32_t cap) {
     __shared__ uint64_t wsum[16];
     const uint32_t e = threadIdx.x, lane = e & 63u, w = e >> 6;
     uint32_t n = 0;
+    int32_t b0 = 0;
     if (e < n_exp) {
-        const int32_t v = bounds[e + 1] - bounds[e];
+        b0 = bounds[e];
+        const int32_t v = bounds[e + 1] - b0;
         n = v > 0 ? (uint32_t)v : 0u;
     }
     const uint32_t nfull = n / mt, tail = n % mt, fcls = mt / 32 - 1;
@@ -120,10 +122,12 @@ __global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ 
     const uint32_t all = cbase[0] + get(total, 0);
     uint32_t start = cbase[fcls] + get(excl, fcls);
     uint32_t k = 0;
-    for (; k < nfull && start + k < cap; k++) tiles[start + k] = make_int2((int)e, (int)(k * mt));
+    // entry: expert, first packed row, rows
+    for (; k < nfull && start + k < cap; k++)
+        tiles[start + k] = make_int4((int)e, b0 + (int)(k * mt), (int)mt, 0);
     if (tcls < 4) {
         const uint32_t at = tcls == fcls ? start + nfull : cbase[tcls] + get(excl, tcls);
-        if (at < cap) tiles[at] = make_int2((int)e, (int)(nfull * mt));
+        if (at < cap) tiles[at] = make_int4((int)e, b0 + (int)(nfull * mt), (int)tail, 0);
     }
     if (e == 0) *count = min(all, cap);
 }
@@ -186,7 +190,7 @@ struct MmqArgs {
     const float *xd;        // [xrows][K/32]
     const int32_t *act_row; // optional: activation row of packed row p
     const int32_t *bounds;  // [n_exp+1]
-    const int2 *tiles;
+    const int4 *tiles;      // (expert, first packed row, rows, -)
     const uint32_t *ntiles;
     uint32_t mt;            // tile height (token rows): 128, 64 or 32
     float *dst;             // plain mode: [rows][ld]
@@ -287,7 +291,7 @@ __device__ inline void mmq_bar_rd() { asm volatile("s_barrier" ::: "memory"); }
 // One (expert, weight block, token tile) of NSUB 32-row token sub-tiles.
 template <uint32_t TY, bool FUSED, int NSUB>
 __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, uint8_t *smem,
-                                                               const int2 tinfo) {
+                                                               const int4 tinfo) {
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
     constexpr uint32_t SB = RawSpec<TY>::SB;
     constexpr uint32_t SSD = RawSpec<TY>::SS / 4;             // raw slot dwords
@@ -299,8 +303,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t e = (uint32_t)tinfo.x;
-    const int32_t rbase = a.bounds[e] + tinfo.y;
-    const uint32_t mrows = min((uint32_t)(a.bounds[e + 1] - rbase), 32u * NSUB);
+    const int32_t rbase = tinfo.y;
+    const uint32_t mrows = min((uint32_t)tinfo.z, 32u * NSUB);
     const uint8_t *We = (a.wx && e == a.ex) ? a.wx : a.w + (uint64_t)e * a.estride;
     // weight row (within the expert) of tile row r
     const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
@@ -311,60 +315,13 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         return We + (uint64_t)wrow(r) * a.rb + (uint64_t)sbi * SB;
     };
 
+    // the codebook entries this thread converts (loaded now, stored into
+    // LDS once the first copies are in flight)
+    uint32_t code[2] = {0u, 0u};
     if (TY == Q4MI_T_IQ3_S) {
-        for (uint32_t i = tid; i < 512; i += 256) {
-            const uint32_t c = q4mi_iq3s_code_dev[i];
-            uint32_t h[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const _Float16 f = (_Float16)(float)(2u * ((c >> (3 * jj)) & 7u) + 1u);
-                h[jj] = __builtin_bit_cast(uint16_t, f);
-            }
-            L.g16[i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        }
-        if (tid < 16) {
-            uint32_t sgn[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) sgn[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
-            L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
-        }
+        code[0] = q4mi_iq3s_code_dev[tid];
+        code[1] = q4mi_iq3s_code_dev[tid + 256];
     }
-    // source rows of this lane's copies: activation op m covers tile rows
-    // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
-    // (rows past the tile's end copy the last row's bytes: their outputs are
-    // never stored, and the copy stays one instruction)
-    const _Float16 *arow_src[NSUB];
-#pragma unroll
-    for (int m = 0; m < NSUB; m++) {
-        const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
-        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
-        const int64_t xr = a.act_row ? a.act_row[p] : p;
-        arow_src[m] = a.xq + (uint64_t)xr * a.K;
-    }
-    const float *drow_src;
-    {
-        const uint32_t r = 32 * wv + lane / 2;
-        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
-        const int64_t xr = a.act_row ? a.act_row[p] : p;
-        drow_src = a.xd + (uint64_t)xr * (a.K / 32);
-    }
-    const uint32_t nsb = a.K / 256;
-    const uint32_t nst = 4 * nsb;                     // 64-value stages
-
-    // copies of stage s (activation codes + scales) into buffer s & 1
-    auto issue_stage = [&](uint32_t s) __attribute__((always_inline)) {
-        const uint32_t buf = s & 1u;
-#pragma unroll
-        for (int m = 0; m < NSUB; m++) {
-            const uint32_t j = wv + 4 * m;            // 8 rows per op
-            const uint32_t r = 8 * j + lane / 8;
-            const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
-            const _Float16 *src = arow_src[m] + s * 64 + c * 8;
-            mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
-        }
-        const float *dsrc = drow_src + s * 2 + (lane & 1u);
-        mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
-    };
     // copies of superblock sbi's raw weight bytes into buffer sbi & 1
     // IQ3_S copy lanes: lane < 29 -> dword `lane` of the first row, 29..57 ->
     // dword lane-29 of the second row (the pad dword re-reads dword 27)
@@ -402,6 +359,44 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         }
     };
 
+    issue_raw(0);   // needs only the expert: goes out before the activation rows resolve
+
+    // source rows of this lane's copies: activation op m covers tile rows
+    // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
+    // (rows past the tile's end copy the last row's bytes: their outputs are
+    // never stored, and the copy stays one instruction)
+    const _Float16 *arow_src[NSUB];
+#pragma unroll
+    for (int m = 0; m < NSUB; m++) {
+        const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
+        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
+        const int64_t xr = a.act_row ? a.act_row[p] : p;
+        arow_src[m] = a.xq + (uint64_t)xr * a.K;
+    }
+    const float *drow_src;
+    {
+        const uint32_t r = 32 * wv + lane / 2;
+        const int32_t p = rbase + (int32_t)min(r, mrows - 1);
+        const int64_t xr = a.act_row ? a.act_row[p] : p;
+        drow_src = a.xd + (uint64_t)xr * (a.K / 32);
+    }
+    const uint32_t nsb = a.K / 256;
+    const uint32_t nst = 4 * nsb;                     // 64-value stages
+
+    // copies of stage s (activation codes + scales) into buffer s & 1
+    auto issue_stage = [&](uint32_t s) __attribute__((always_inline)) {
+        const uint32_t buf = s & 1u;
+#pragma unroll
+        for (int m = 0; m < NSUB; m++) {
+            const uint32_t j = wv + 4 * m;            // 8 rows per op
+            const uint32_t r = 8 * j + lane / 8;
+            const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
+            const _Float16 *src = arow_src[m] + s * 64 + c * 8;
+            mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
+        }
+        const float *dsrc = drow_src + s * 2 + (lane & 1u);
+        mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
+    };
     f32x16_t acc[NSUB], inner[NSUB];
 #pragma unroll
     for (int t = 0; t < NSUB; t++) {
@@ -409,8 +404,26 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         inner[t] = f32x16_t{};
     }
     const uint32_t arow = 32 * wv + (lane & 31u);    // this lane's weight row in the tile
-    issue_raw(0);
     issue_stage(0);
+    if (TY == Q4MI_T_IQ3_S) {   // IQ3_S tables (read after the first barrier pair)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; h2++) {
+            const uint32_t c = code[h2];
+            uint32_t h[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const _Float16 f = (_Float16)(float)(2u * ((c >> (3 * jj)) & 7u) + 1u);
+                h[jj] = __builtin_bit_cast(uint16_t, f);
+            }
+            L.g16[tid + 256 * h2] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        }
+        if (tid < 16) {
+            uint32_t sgn[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) sgn[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
+            L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
+        }
+    }
     for (uint32_t s = 0; s < nst; s++) {
         const uint32_t sbi = s >> 2, q = s & 3u;
         // the row's raw bytes start at the same offset inside its slot as
@@ -584,9 +597,9 @@ template <uint32_t TY, bool FUSED>
 __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t ti = blockIdx.y;
+    const int4 tinfo = a.tiles[ti];          // in bounds: the grid is the list's capacity
     if (ti >= *a.ntiles) return;
-    const int2 tinfo = a.tiles[ti];
-    const int32_t rows = min(a.bounds[tinfo.x + 1] - a.bounds[tinfo.x] - tinfo.y, (int32_t)a.mt);
+    const int32_t rows = tinfo.z;
     // block-uniform choice of the (branch-free) sub-tile count
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
     case 4: mmq_tile<TY, FUSED, 4>(a, smem, tinfo); break;
@@ -596,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     }
 }
 
-static int2 *g_tiles = nullptr;
+static int4 *g_tiles = nullptr;
 static uint32_t *g_ntiles = nullptr;
 static uint32_t g_tiles_cap = 0;
 
@@ -604,7 +617,7 @@ static bool ensure_tiles(uint32_t n) {
     if (g_tiles_cap >= n) return true;
     if (g_tiles) (void)hipFree(g_tiles);
     if (!g_ntiles && hipMalloc(&g_ntiles, sizeof(uint32_t)) != hipSuccess) return false;
-    if (hipMalloc(&g_tiles, (size_t)n * sizeof(int2)) != hipSuccess) {
+    if (hipMalloc(&g_tiles, (size_t)n * sizeof(int4)) != hipSuccess) {
         g_tiles = nullptr;
         g_tiles_cap = 0;
         return false;
