@@ -108,6 +108,28 @@ bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_
                          uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
                          const float *d_x, float *d_h, float *d_y, uint32_t n_ff,
                          uint32_t in_dim, uint32_t n_embd);
+/* Per-token small batch: token t's picks at d_slots/d_wts[h_off[t] ..
+ * h_off[t+1]) (device arrays, host prefix offsets), x and y token-major, y
+ * accumulated; nothing is queued when false is returned.  Equal counts run
+ * as one window.  d_h, d_h2 unused.  Replaces q4_hip_moe_tok_ok /
+ * q4_hip_moe_exec_tok (src/q4.h:893-901, src/q4_rocm.cu:5606-5657). */
+bool q4_hip_moe_tok_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uint32_t n_ff);
+bool q4_hip_moe_exec_tok(const uint8_t *base, uint64_t stride, const int32_t *d_slots,
+                         const float *d_wts, const uint32_t *h_off, uint32_t n_tok, uint32_t gt,
+                         uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
+                         const float *d_x, float *d_h, float *d_h2, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd);
+/* Staged list for graphs: q4_hip_moe_stage copies one token's host list
+ * (n <= 64) into pinned memory; q4_hip_moe_exec_staged is q4_hip_moe_exec_dev
+ * over that memory, read when the kernels run, so a captured graph replays
+ * with the list staged last.  Do not restage while a launch reading the
+ * previous list is queued.  Replaces q4_hip_moe_stage /
+ * q4_hip_moe_exec_staged (src/q4.h:1306-1311, src/q4_rocm.cu:7548-7590). */
+bool q4_hip_moe_stage(const int32_t *slots, const float *wts, uint32_t n);
+bool q4_hip_moe_exec_staged(const uint8_t *base, uint64_t stride, uint32_t gt, uint64_t og,
+                            uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
+                            const float *d_x, float *d_h, float *d_h2, float *d_down,
+                            float *d_y, uint32_t n_ff, uint32_t in_dim, uint32_t n_embd);
 
 /* ------------------------------------------------------ routing and pack */
 
@@ -148,9 +170,9 @@ bool q4_hip_expert_reduce(float *d_y, const float *d_pd, const int32_t *d_rsrc,
  * to the next 4-byte boundary after their last byte (any hipMalloc'd
  * buffer is).  The activation buffer layout is this
  * library's (q4_mmq_q8_bytes gives its size); its codes are the bit-exact
- * CPU-expert q8 codes.  The slot-gather helpers (q4_mmq_wbuf*, q4_mmq_gather,
- * q4_mmq_pad) have no counterpart: every expert is resident and MMQ reads it
- * in place at w + e*expert_stride_bytes. */
+ * CPU-expert q8 codes.  With every expert resident, MMQ reads it in place at
+ * w + e*expert_stride_bytes; the expert-gather helpers below serve engines
+ * that still stage experts. */
 int q4_mmq_on(void);
 uint32_t q4_mmq_group(void);
 bool q4_mmq_supported(uint32_t type, uint64_t w_rows);
@@ -162,6 +184,26 @@ bool q4_mmq_mul_id(const void *w, uint32_t type, uint64_t w_rows, uint64_t w_col
                    const int32_t *bounds, uint32_t max_rows, uint64_t total_rows, float *dst,
                    uint64_t ld_dst);
 bool q4_mmq_swiglu(const float *gu, float *h, uint64_t rows, uint64_t n_ff);
+/* Expert-id-indexed weight buffers (src/q4.h:1161-1174,
+ * src/q4_mmq.cu:447-601).  q4_mmq_pad: guard bytes after each gathered
+ * expert, 0 here (no kernel reads past an expert's rows).  q4_mmq_wbuf:
+ * library buffers of n_exp*gu_bytes and n_exp*d_bytes, grown and zeroed on
+ * demand (allocates: not during capture).  q4_mmq_wbuf_lend: use caller
+ * memory instead (zeroed; NULL drops it) from then on.  q4_mmq_gather: for
+ * i < n, slot d_slot[i]'s [goff, +gu_bytes) and [doff, +d_bytes) go to
+ * d_gu + d_eid[i]*gu_dst and d_d + d_eid[i]*d_dst, tails zeroed up to the
+ * strides.  q4_mmq_wbuf_size / q4_mmq_wbuf_need read the reference's model
+ * struct and are not provided: the sizes are 2*n_ff rows of the gate type
+ * and n_embd rows of the down type (IQ3_S 110 B per 256 values, Q8_0 34 B
+ * per 32). */
+uint64_t q4_mmq_pad(uint64_t row_bytes);
+bool q4_mmq_wbuf(uint64_t gu_bytes, uint64_t d_bytes, uint32_t n_exp, uint8_t **gu,
+                 uint8_t **d);
+bool q4_mmq_wbuf_lend(void *gu, uint64_t gu_bytes, void *d, uint64_t d_bytes);
+bool q4_mmq_gather(const uint8_t *abase, uint64_t astride, uint64_t goff, uint64_t gu_bytes,
+                   uint64_t doff, uint64_t d_bytes, uint64_t gu_dst, uint64_t d_dst,
+                   const int32_t *d_eid, const int32_t *d_slot, uint32_t n, uint8_t *d_gu,
+                   uint8_t *d_d);
 /* q4_mmq_mul_id with activation rows gathered through act_row: xq holds
  * xrows rows (one per token, quantized once) and packed row p reads row
  * act_row[p] (the pack's a_tok).  No reference counterpart: it removes the

@@ -31,6 +31,7 @@
 // (2s+1) multiplier on the exact int32 group sum, and float(S) * (d_w * d_x).
 #include <stddef.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -1050,6 +1051,36 @@ using namespace q4mi;
 
 extern "C" void q4_mmvq_warm(void);
 
+// Staged expert list for q4_hip_moe_stage / q4_hip_moe_exec_staged: coherent
+// pinned host memory that the host rewrites per token and the kernels read
+// through its device alias when they run (so a captured graph replays with
+// the list staged last).
+struct StageList {
+    int32_t id[kMaxU];
+    float w[kMaxU];
+    int32_t n;
+};
+static StageList *g_stage = nullptr, *g_stage_dev = nullptr;
+
+static bool stage_ready() {
+    if (g_stage) return true;
+    void *p = nullptr, *dp = nullptr;
+    if (hipHostMalloc(&p, sizeof(StageList), hipHostMallocMapped | hipHostMallocCoherent) !=
+        hipSuccess) {
+        set_error("q4_hip_moe_stage: pinned allocation failed");
+        return false;
+    }
+    if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess) {
+        (void)hipHostFree(p);
+        set_error("q4_hip_moe_stage: no device alias for the staging list");
+        return false;
+    }
+    memset(p, 0, sizeof(StageList));
+    g_stage = (StageList *)p;
+    g_stage_dev = (StageList *)dp;
+    return true;
+}
+
 extern "C" {
 
 /* Benchmark hook: 1 = gate/up launch only, 2 = down only, 3 = both. */
@@ -1062,6 +1093,7 @@ void q4mi_moe_lds_cap(uint32_t bytes) { g_lds_cap = bytes; }
 /* Allocate the decode scratch (call before any stream capture). */
 void q4_hip_moe_scratch_warm(void) {
     (void)moe_warm(1024);
+    (void)stage_ready();
     q4_mmvq_warm();
 }
 /* One token, n (<=64) experts given as HOST arrays: slot ids (expert index
@@ -1146,6 +1178,86 @@ bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_
     ListSrc src = {d_es, d_ew, d_nh, kMaxU, n_tok, 0, 0};
     return moe_run(base, stride, src, hl, 0, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
                    n_embd);
+}
+
+/* Per-token small-batch preflight: the type/shape rule of the exec calls. */
+bool q4_hip_moe_tok_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uint32_t n_ff) {
+    return gt == ut && type_ok(gt, in_dim) && type_ok(dt, n_ff) && n_ff <= 1024;
+}
+
+/* n_tok tokens; token t's picks are d_slots/d_wts[h_off[t] .. h_off[t+1])
+ * (device arrays, host offsets); x and y token-major, y accumulated.
+ * Everything is checked before the first launch.  Equal counts (2..8
+ * tokens, at most 64 picks in all) run as one window; otherwise one
+ * device-list layer per token. */
+bool q4_hip_moe_exec_tok(const uint8_t *base, uint64_t stride, const int32_t *d_slots,
+                         const float *d_wts, const uint32_t *h_off, uint32_t n_tok, uint32_t gt,
+                         uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
+                         const float *d_x, float *d_h, float *d_h2, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd) {
+    (void)d_h;
+    (void)d_h2;
+    if (!d_slots || !d_wts || !h_off || !n_tok) {
+        set_error("q4_hip_moe_exec_tok: bad arguments");
+        return false;
+    }
+    if (!q4_hip_moe_tok_ok(gt, ut, dt, in_dim, n_ff) || n_embd != in_dim) {
+        set_error("q4_hip_moe_exec_tok: types/shape not covered");
+        return false;
+    }
+    const uint32_t c0 = h_off[1] - h_off[0];
+    bool same = n_tok >= 2 && n_tok <= kMaxT;
+    for (uint32_t t = 0; t < n_tok; t++) {
+        if (h_off[t + 1] < h_off[t] || h_off[t + 1] - h_off[t] > kMaxU) {
+            set_error("q4_hip_moe_exec_tok: token %u has a bad pick range", t);
+            return false;
+        }
+        same = same && h_off[t + 1] - h_off[t] == c0;
+    }
+    if (h_off[n_tok] == h_off[0]) return true;
+    HostList hl = {};
+    if (same && (uint64_t)c0 * n_tok <= kMaxU) {
+        ListSrc src = {d_slots + h_off[0], d_wts + h_off[0], nullptr, c0, n_tok, c0, 0};
+        return moe_run(base, stride, src, hl, 0, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
+                       n_embd);
+    }
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const uint32_t cnt = h_off[t + 1] - h_off[t];
+        if (!cnt) continue;
+        ListSrc src = {d_slots + h_off[t], d_wts + h_off[t], nullptr, cnt, 1, cnt, 0};
+        if (!moe_run(base, stride, src, hl, cnt, gt, og, ut, ou, dt, od,
+                     d_x + (size_t)t * in_dim, d_y + (size_t)t * n_embd, n_ff, in_dim, n_embd))
+            return false;
+    }
+    return true;
+}
+
+/* Stage one token's list (n <= 64 slot ids and weights, host arrays) for
+ * q4_hip_moe_exec_staged.  The caller must not restage while a launch that
+ * reads the previous list is still queued. */
+bool q4_hip_moe_stage(const int32_t *slots, const float *wts, uint32_t n) {
+    if ((n && (!slots || !wts)) || n > kMaxU) {
+        set_error("q4_hip_moe_stage: bad expert list");
+        return false;
+    }
+    if (!stage_ready()) return false;
+    for (uint32_t i = 0; i < n; i++) {
+        g_stage->id[i] = slots[i];
+        g_stage->w[i] = wts[i];
+    }
+    g_stage->n = (int32_t)n;
+    return true;
+}
+
+/* q4_hip_moe_exec_dev over the staged list, read when the kernels run. */
+bool q4_hip_moe_exec_staged(const uint8_t *base, uint64_t stride, uint32_t gt, uint64_t og,
+                            uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
+                            const float *d_x, float *d_h, float *d_h2, float *d_down,
+                            float *d_y, uint32_t n_ff, uint32_t in_dim, uint32_t n_embd) {
+    if (!stage_ready()) return false;
+    return q4_hip_moe_exec_dev(base, stride, g_stage_dev->id, g_stage_dev->w, &g_stage_dev->n,
+                               gt, og, ut, ou, dt, od, d_x, d_h, d_h2, d_down, d_y, n_ff, in_dim,
+                               n_embd);
 }
 
 }  // extern "C"

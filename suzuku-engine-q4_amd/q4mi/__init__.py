@@ -53,6 +53,12 @@ _SIGS = {
     "q4_hip_moe_win_ok": (_b, [_u32, _u32, _u32, _u32, _u32, _u32]),
     "q4_hip_moe_exec_win": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
                                  _u64, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_moe_tok_ok": (_b, [_u32, _u32, _u32, _u32, _u32]),
+    "q4_hip_moe_exec_tok": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
+                                 _u64, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_moe_stage": (_b, [_vp, _vp, _u32]),
+    "q4_hip_moe_exec_staged": (_b, [_vp, _u64, _u32, _u64, _u32, _u64, _u32, _u64, _vp, _vp,
+                                    _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_route_pf": (_b, [_vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_softmax_topk_launch": (_b, [_vp, _u32, _u32, _vp, _vp]),
     "q4_hip_softmax_topk": (_b, [_vp, _u32, _u32, _vp, _vp]),
@@ -66,6 +72,11 @@ _SIGS = {
     "q4_mmq_quantize": (_b, [_vp, _vp, _vp, _u32, _u64, _u64]),
     "q4_mmq_mul_id": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _vp, _u32, _u64, _vp, _u64]),
     "q4_mmq_swiglu": (_b, [_vp, _vp, _u64, _u64]),
+    "q4_mmq_pad": (_u64, [_u64]),
+    "q4_mmq_wbuf": (_b, [_u64, _u64, _u32, _vp, _vp]),
+    "q4_mmq_wbuf_lend": (_b, [_vp, _u64, _vp, _u64]),
+    "q4_mmq_gather": (_b, [_vp, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _vp, _vp, _u32, _vp,
+                           _vp]),
     "q4mi_mmq_mul_id_rows": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp, _u64,
                                   _vp, _u64]),
     "q4mi_mmq_gate_up": (_b, [_vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp, _vp, _u64,

@@ -70,3 +70,25 @@ def test_loads_and_rejects_without_gpu():
                                  16, 512, 2048, 2048)
     assert not L.q4_hip_moe_exec(1, 0, ids, w, 0, 21, 0, 21, 0, 21, 0, 16, None, None, None,
                                  16, 512, 2048, 2048)
+
+
+def test_boundary_extras_reject_without_gpu():
+    """The staged / per-token decode and MMQ gather entry points check their
+    arguments on the host before any device work."""
+    L = q4mi.lib()
+    T = q4mi.T_IQ3_S
+    assert L.q4_hip_moe_tok_ok(T, T, T, 2048, 512)
+    assert not L.q4_hip_moe_tok_ok(T, q4mi.T_Q8_0, T, 2048, 512)
+    assert not L.q4_hip_moe_tok_ok(T, T, T, 2048, 2048)
+    off = (ctypes.c_uint32 * 3)(0, 70, 70)          # token 0: 70 picks > 64
+    assert not L.q4_hip_moe_exec_tok(1, 1, 1, 1, off, 2, T, 0, T, 0, T, 0, 16, None, None, 16,
+                                     512, 2048, 2048)
+    assert "pick range" in q4mi.last_error()
+    assert not L.q4_hip_moe_exec_tok(1, 1, 1, 1, off, 2, T, 0, T, 0, T, 0, 16, None, None, 16,
+                                     512, 2048, 1024)   # n_embd != in_dim
+    assert not L.q4_hip_moe_stage(None, None, 65)
+    assert L.q4_mmq_pad(880) == 0
+    # destination stride below the slice size
+    assert not L.q4_mmq_gather(1, 0, 0, 100, 0, 100, 50, 100, 1, 1, 1, 1, 1)
+    assert L.q4_mmq_gather(None, 0, 0, 0, 0, 0, 0, 0, None, None, 0, None, None)   # n = 0
+    assert not L.q4_mmq_wbuf(1, 1, 0, None, None)
