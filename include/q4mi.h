@@ -193,9 +193,7 @@ bool q4_mmq_swiglu(const float *gu, float *h, uint64_t rows, uint64_t n_ff);
  * i < n, slot d_slot[i]'s [goff, +gu_bytes) and [doff, +d_bytes) go to
  * d_gu + d_eid[i]*gu_dst and d_d + d_eid[i]*d_dst, tails zeroed up to the
  * strides.  q4_mmq_wbuf_size / q4_mmq_wbuf_need read the reference's model
- * struct and are not provided: the sizes are 2*n_ff rows of the gate type
- * and n_embd rows of the down type (IQ3_S 110 B per 256 values, Q8_0 34 B
- * per 32). */
+ * struct and stay in the host engine. */
 uint64_t q4_mmq_pad(uint64_t row_bytes);
 bool q4_mmq_wbuf(uint64_t gu_bytes, uint64_t d_bytes, uint32_t n_exp, uint8_t **gu,
                  uint8_t **d);
