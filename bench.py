@@ -236,6 +236,9 @@ def main():
                      "traffic": measured_traffic("moe_gu_k"),
                      "kernel": "moe_gu_k", "bytes_per_launch": GU_BYTES},
     }
+    if not args.no_extra:
+        out["config3_window"] = bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
+                                             capture, timed, args)
     del g_full, g_gu, g_dn, arenas
     torch.cuda.empty_cache()
 
@@ -334,6 +337,58 @@ def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
             "weight_GB_per_s": round(wbytes / t / 1e9, 1),
             "note": "whole routed layer incl. route, pack, quantize, SwiGLU, reduce and the "
                     "shared expert; ops = (20480 + 2048) rows x 3 x 2048 x 512 x 2"}
+
+
+def bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, timed, args,
+                 n_tok=4):
+    """Config 3: the 4-token verify window (1 accepted + 3 drafted tokens, each
+    with its own top-10 from seeded N(0,1) logits, plus the shared expert)
+    sustained over the same stack of distinct-expert layers.  Bytes per layer
+    = every unique expert once (the window reads each expert once for all of
+    its tokens) + x and y."""
+    rng = np.random.default_rng(4321)
+    es = np.full((NL, n_tok, 64), -1, np.int32)
+    ew = np.zeros((NL, n_tok, 64), np.float32)
+    nh = np.zeros((NL, n_tok), np.int32)
+    uniq = []
+    for l in range(NL):
+        ids_l = set()
+        for t, (ids, w) in enumerate(routes(rng, n_tok)):
+            es[l, t, :len(ids)], ew[l, t, :len(ids)], nh[l, t] = ids, w, len(ids)
+            ids_l.update(int(i) for i in ids)
+        uniq.append(len(ids_l))
+    d_es, d_ew, d_nh = (torch.from_numpy(a).cuda() for a in (es, ew, nh))
+    xs = torch.randn(NL, n_tok, N_EMBD, device="cuda",
+                     generator=torch.Generator("cuda").manual_seed(10))
+    ys = torch.zeros(NL, n_tok, N_EMBD, device="cuda")
+    T = q4mi.T_IQ3_S
+
+    def stack():
+        for l in range(NL):
+            q4mi.check(L.q4_hip_moe_exec_win(arenas[l].data_ptr(), stride, d_es[l].data_ptr(),
+                                             d_ew[l].data_ptr(), d_nh[l].data_ptr(), n_tok, T,
+                                             og, T, ou, T, od, xs[l].data_ptr(), None,
+                                             ys[l].data_ptr(), N_FF, N_EMBD, N_EMBD),
+                       "q4_hip_moe_exec_win")
+    g = capture(stack)
+    ys.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    y_graph = ys.clone()
+    ys.zero_()
+    stack()
+    torch.cuda.synchronize()
+    assert torch.equal(y_graph, ys), "window graph replay differs from eager"
+    steps = max(args.steps // 4, 10)
+    ms = timed(g, steps, max(args.warmup // 4, 2))
+    t = ms * 1e-3 / (steps * NL)
+    nbytes = float(np.mean(uniq)) * EXPERT_BYTES + 2 * 4 * n_tok * N_EMBD
+    del g
+    return {"layer_us": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+            "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
+            "unique_experts": round(float(np.mean(uniq)), 2), "tokens": n_tok,
+            "note": "4 tokens, own top-10 each + shared; each unique expert read once; "
+                    "graph over the %d-layer stack" % NL}
 
 
 def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):

@@ -84,10 +84,13 @@ struct __align__(16) Plan {
 // (token, pick)); callers sync afterwards.
 __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
     // lane -> (token, pick) of the flattened lists, token-major
+    // every token's count in one load (lane t holds token t's), then
+    // read back lane by lane: one memory round trip, not one per token
+    const int cnt_l = lane < s.n_tok ? (s.nh ? s.nh[lane] : (int)s.n_fixed) : 0;
     uint32_t E = 0, tok = 0, rem = 0;
     bool found = false;
     for (uint32_t t = 0; t < s.n_tok; t++) {
-        int c = s.nh ? s.nh[t] : (int)s.n_fixed;
+        int c = __builtin_amdgcn_readlane(cnt_l, t);
         if (c < 0) c = 0;
         if ((uint32_t)c > s.stride) c = (int)s.stride;
         if (!found && lane < E + (uint32_t)c) {
@@ -105,11 +108,14 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
         w = s.ew[(size_t)tok * s.stride + rem];
     }
     const bool valid = lane < E && id >= 0;
+    // first occurrence of each id: lane reads (v_readlane, a few cycles)
+    // instead of lane shuffles (an LDS round trip each)
+    const uint64_t vmask = __ballot(valid);
     uint32_t first_j = lane;
     for (uint32_t j = 0; j < E; j++) {
-        const int32_t idj = __shfl(id, j);
-        const bool vj = __shfl((int)valid, j) != 0;
-        if (vj && idj == id && j < first_j) first_j = j;
+        if (!((vmask >> j) & 1ull)) continue;
+        const int32_t idj = __builtin_amdgcn_readlane(id, j);
+        if (idj == id && j < first_j) first_j = j;
     }
     const bool first = valid && first_j == lane;
     const uint64_t fm = __ballot(first);
@@ -531,7 +537,18 @@ __device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, 
     const float4 *xg = (const float4 *)a.x;
     if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, xq, xd);
-    for (uint32_t i = ct + kCons; i < nq; i += kCons) quant_quad(xg[i], i, xq, xd);
+    // further quads (several tokens) four loads in flight at a time
+    for (uint32_t i0 = ct + kCons; i0 < nq; i0 += 4 * kCons) {
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t i = i0 + k * kCons;
+            v[k] = i < nq ? xg[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (i0 + k * kCons < nq) quant_quad(v[k], i0 + k * kCons, xq, xd);
+    }
     if (lane == 0) atomicAdd(&Y->ready, 1u);
     spin_ge(&Y->ready, kConsW);                     // table and q8(x) complete
     Q4MI_TR(4, 0, ct == 0);
@@ -710,7 +727,18 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
     if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, hq, hd);
     if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
-    for (uint32_t i = ct + 2 * kCons; i < nq; i += kCons) quant_quad(*hquad(i), i, hq, hd);
+    // further quads (many pairs) eight loads in flight at a time
+    for (uint32_t i0 = ct + 2 * kCons; i0 < nq; i0 += 8 * kCons) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t i = i0 + k * kCons;
+            v[k] = i < nq ? *hquad(i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + k * kCons < nq) quant_quad(v[k], i0 + k * kCons, hq, hd);
+    }
     if (lane == 0) atomicAdd(&Y->ready, 1u);
     spin_ge(&Y->ready, kConsW);                     // table and q8(h) complete
     Q4MI_TR(4, 1, ct == 0);
@@ -907,9 +935,12 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
 }
 
 // Gate/up lanes per pair: 32 (two or more groups per lane, two pairs per
-// wave) while the activation registers stay small, else the row layout.
+// wave, so each wave has two pairs' chains in flight) while the activation
+// registers stay small (groups x tokens <= 4, or 2 groups x 4 tokens), else
+// the row layout.
 static RowLayout gu_layout(uint32_t G, int NT) {
-    if (G >= 64 && G % 32 == 0 && (G / 32) * (uint32_t)NT <= 4) return RowLayout{32, (int)(G / 32)};
+    const uint32_t gn = (G / 32) * (uint32_t)NT;
+    if (G >= 64 && G % 32 == 0 && (gn <= 4 || (NT == 4 && G == 64))) return RowLayout{32, (int)(G / 32)};
     return layout_for(G);
 }
 
@@ -919,7 +950,7 @@ static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_gu<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
-    if constexpr (NT <= 2) { Q4MI_L(32, 2) }
+    if constexpr (NT <= 4) { Q4MI_L(32, 2) }
     if constexpr (NT == 1) { Q4MI_L(32, 4) }
 #undef Q4MI_L
     return false;
@@ -929,7 +960,7 @@ static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
 // 96 teams cover a block's (expert, row) items in one round; else the row
 // layout.
 static RowLayout dn_layout(uint32_t G, int NT) {
-    if (G == 16 && NT <= 2) return RowLayout{8, 2};
+    if (G == 16 && NT <= 4) return RowLayout{8, 2};
     return layout_for(G);
 }
 
@@ -939,7 +970,7 @@ static bool dn_dispatch(const MoeArgs &a, uint32_t nu_host) {
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_dn<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
-    if constexpr (NT <= 2) { Q4MI_L(8, 2) }
+    if constexpr (NT <= 4) { Q4MI_L(8, 2) }
 #undef Q4MI_L
     return false;
 }
