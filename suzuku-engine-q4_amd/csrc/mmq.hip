@@ -3,8 +3,9 @@
 // Routed rows are packed per expert (ragged bounds[e]..bounds[e+1]).  For
 // each (expert, 128-row token tile, 128-row weight tile) a 256-thread block
 // walks K one IQ3_S superblock (256 values) at a time:
-//   * weights: IQ3_S -> exact integers w*(2s+1) (|v| <= 465), written to LDS
-//     as fp16 (exact); Q8_0 -> its int8 values as fp16 (exact);
+//   * weights: the raw blocks are copied to LDS; each lane decodes its MFMA
+//     operands in registers: IQ3_S -> exact integers w*(2s+1) (|v| <= 465)
+//     as fp16; Q8_0 -> its int8 values as fp16;
 //   * activations: q8 codes (exact fp16 copies made by the quantizer) and
 //     their fp32 group scales;
 //   * per 32-value group: two v_mfma_f32_32x32x16_f16 produce the exact
@@ -137,17 +138,17 @@ __global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ 
 // Wave w owns weight rows [32w, 32w+32) of the tile and every token of it
 // (four 32-token sub-tiles, skipped when empty).  Each K superblock:
 //   1. the 128 rows' raw block bytes are copied to LDS with dword loads;
-//   2. per half superblock the 128 token rows' fp16 codes are copied to LDS;
+//   2. per 64-value stage the 128 token rows' fp16 codes (and group scales)
+//      are copied to LDS, double-buffered;
 //   3. per 32-value group each lane decodes the 16 weight values its MFMA A
 //      operand needs straight from the raw bytes (lane half kh takes values
 //      8kh..8kh+7 and 16+8kh..+7), then two 32x32x16 MFMAs per token sub-tile.
 // Fused gate/up mode: tile rows 0..63 are gate rows n0..n0+63 and 64..127
-// the matching up rows F+n0..; waves 2,3 hand their accumulators to waves
-// 0,1 through LDS, which form h = silu(g)*u and write its q8 codes (the
-// 32 h columns of a q8 group are in the lane and its partner lane l^32).
+// the matching up rows F+n0..; each gate/up wave pair (w, w+2) exchanges
+// half of its accumulators through LDS, and each wave forms h = silu(g)*u
+// and its q8 codes for half of the token sub-tiles (the 32 h columns of a
+// q8 group are in the lane and its partner lane l^32).
 constexpr int MMQ_NB = 128;      // weight rows per block
-// token sub-tiles whose MFMA chains are interleaved (two measured no faster
-// than one, and one keeps the register budget clear of spills)
 constexpr int MMQ_MB = 128;      // token rows per block
 
 // Raw superblock slots in LDS.  A row's slot holds the dwords covering its
