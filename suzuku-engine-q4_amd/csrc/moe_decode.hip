@@ -14,14 +14,17 @@
 // q4_hip_moe_exec_win src/q4_rocm.cu:7444-7531, CPU twin
 // q4_cpuex_dispatch_win src/q4_cpuexp.c:2618-2753).
 //
-// Memory pipeline (both kernels): every byte a block needs is copied
-// HBM -> LDS with gfx950 global_load_lds (no registers).  A prologue copies
-// the small inputs (IQ3_S code table, x or h, y), then the block's weight
-// rows are issued as up to S chunks into an LDS ring before anything waits.
-// VMEM loads of a wave complete in issue order, so a wave waits for chunk c
-// with s_waitcnt vmcnt(#loads it issued after chunk c) and a plain s_barrier
-// makes every wave's part visible: chunk c is computed while chunks c+1..
-// are still in flight, and no wait ever covers more than it needs.
+// Memory pipeline (both kernels), after the block's single barrier:
+//   producers (waves 0..kProd-1) issue the block's weight rows as chunks
+//     into an LDS ring with gfx950 global_load_lds (no registers) and
+//     publish each chunk (landed[] in LDS) once its own copies are complete,
+//     waiting with s_waitcnt vmcnt(#copies issued after it): VMEM loads of a
+//     wave complete in issue order, so no wait covers more than it needs;
+//     a slot is refilled only after its previous chunk was consumed;
+//   consumers (the other waves) load the codebook and x (or h) through
+//     registers in the prologue, build the signed table and the q8
+//     activations in LDS, then compute each (expert, row) item as soon as
+//     its chunk is published and count it consumed (cons[] in LDS).
 //
 // IQ3_S decode: one LDS lookup per 4 values into an 8192-entry table of
 // signed int8 quads (index = sign nibble << 9 | qh bit << 8 | qs byte), built
