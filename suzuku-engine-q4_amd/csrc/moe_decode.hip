@@ -311,6 +311,8 @@ struct MoeArgs {
 #ifdef Q4MI_TRACE
     unsigned long long *trace;   // [2 kernels][4096 blocks][32] phase timestamps
 #endif
+    Plan *gplan;      // device list: the plan gate/up block 0 publishes for down
+    uint32_t plan_in; // down: load gplan instead of building the plan
     HostList hl;      // host list (src.unique), read in place from the kernel arguments
 };
 
@@ -499,6 +501,10 @@ __device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, 
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
     if (!uniq && tid < 64) build_plan(P, a.src, tid);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    if (!uniq && bid == 0 && wave == kProd) {   // the down launch reuses this plan
+        for (uint32_t i = lane; i < sizeof(Plan) / 16; i += 64)
+            ((uint4 *)a.gplan)[i] = ((const uint4 *)P)[i];
+    }
     const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
     const uint32_t PT = nu * n_ff;
     const uint32_t p0 = (uint32_t)(((uint64_t)PT * bid) / nblk);
@@ -677,7 +683,14 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
         }
     }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) build_plan(P, a.src, tid);
+    if (!uniq && tid < 64) {
+        if (a.plan_in) {   // the plan the gate/up launch of this call published
+            for (uint32_t i = tid; i < sizeof(Plan) / 16; i += 64)
+                ((uint4 *)P)[i] = ((const uint4 *)a.gplan)[i];
+        } else {
+            build_plan(P, a.src, tid);
+        }
+    }
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
     const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
     const uint32_t nsel = uniq ? nu : P->nsel;
@@ -1018,7 +1031,13 @@ static bool shape_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uin
            n_ff <= 1024;
 }
 
+static Plan *g_plan = nullptr;   // a device-list call's plan, gate/up -> down
+
 bool moe_warm(uint32_t n_ff) {
+    if (!g_plan && hipMalloc(&g_plan, sizeof(Plan)) != hipSuccess) {
+        set_error("moe: plan buffer allocation failed");
+        return false;
+    }
     // fp32 h of every (unique expert, token) pair
     return ensure_pd((size_t)kMaxU * kMaxT * n_ff);
 }
@@ -1067,6 +1086,8 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     a.y = d_y;
     a.src = src;
     a.hl = hl;
+    a.gplan = g_plan;
+    a.plan_in = (g_phases & 1) ? 1u : 0u;   // down follows this call's gate/up
 #ifdef Q4MI_TRACE
     if (!g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
         (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
