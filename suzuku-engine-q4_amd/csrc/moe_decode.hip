@@ -134,9 +134,9 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (first) P->uid[u] = id;
-    if (valid) {
+    if (valid) {   // a token's repeated id adds its weights
         atomicOr(&P->sel[u], 1u << tok);
-        P->w[tok][u] = w;
+        atomicAdd(&P->w[tok][u], w);
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
@@ -1167,16 +1167,20 @@ bool q4_hip_moe_exec(const uint8_t *base, uint64_t stride, const int32_t *slots,
         set_error("q4_hip_moe_exec: bad expert list");
         return false;
     }
-    // unique ids in first-appearance order; a repeated id keeps the weight
-    // of its last occurrence (the device plan's rule for device lists)
+    // unique ids in first-appearance order; a repeated id adds its weights
+    // (the reference computes every entry and sums them)
     HostList hl;
     uint32_t nu = 0;
     for (uint32_t i = 0; i < n; i++) {
         if (slots[i] < 0) continue;
         uint32_t u = 0;
         while (u < nu && hl.id[u] != slots[i]) u++;
-        if (u == nu) hl.id[nu++] = slots[i];
-        hl.w[u] = wts[i];
+        if (u == nu) {
+            hl.id[nu++] = slots[i];
+            hl.w[u] = wts[i];
+        } else {
+            hl.w[u] += wts[i];
+        }
     }
     for (uint32_t i = nu; i < kMaxU; i++) {
         hl.id[i] = -1;

@@ -398,3 +398,34 @@ def test_moe_decode_seed_sweep(gpu, oracle):
             yp += wts[j] * oracle.dot8_rows(T_IQ3_S, wd, ly.n_embd, ly.n_ff, hj[None])[0]
         assert layer_err(y, yo) <= max(TOL, 2 * layer_err(yp, yo)), seed
     assert ties <= 2
+
+
+def test_moe_repeated_ids_and_64_experts(gpu, oracle):
+    """A token list with repeated ids counts each entry (the reference
+    computes every entry of the list and sums them), on the host-list and
+    device-list paths; and the 64-expert maximum of one call."""
+    ly = layer()
+    rng = np.random.default_rng(81)
+    x = rng.standard_normal(ly.n_embd).astype(np.float32)
+    cases = [(np.array([5, 9, 5, 512, 9, 5], np.int32),
+              np.array([0.3, 0.2, 0.4, 1.0, 0.1, 0.05], np.float32))]
+    ids64 = rng.choice(512, 63, replace=False).astype(np.int32)
+    w64 = rng.random(63).astype(np.float32)
+    cases.append((np.append(ids64, 512).astype(np.int32),
+                  np.append(w64 / w64.sum(), 1.0).astype(np.float32)))
+    for ids, wts in cases:
+        yo = oracle.moe_tokens(ly.n_embd, ly.n_ff, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x,
+                               ids[None], wts[None])[0]
+        y = moe_exec_host(gpu, ly, x, ids, wts)
+        assert rel_err(y, yo) <= TOL, len(ids)
+        es = np.full(64, -1, np.int32)
+        ew = np.zeros(64, np.float32)
+        es[:len(ids)], ew[:len(ids)] = ids, wts
+        d_es, d_ew, d_n = dev(es), dev(ew), dev(np.array([len(ids)], np.int32))
+        dx, yd = dev(x), dev(np.zeros(ly.n_embd, np.float32))
+        q4mi.check(gpu.q4_hip_moe_exec_dev(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es),
+                                           q4mi.ptr(d_ew), q4mi.ptr(d_n), T_IQ3_S, ly.og, T_IQ3_S,
+                                           ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx), None, None, None,
+                                           q4mi.ptr(yd), ly.n_ff, ly.n_embd, ly.n_embd),
+                   "q4_hip_moe_exec_dev")
+        assert rel_err(host(yd), yo) <= TOL, len(ids)
