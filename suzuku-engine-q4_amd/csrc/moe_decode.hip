@@ -421,9 +421,9 @@ __device__ inline void wait_chunk(const Sync *y, uint32_t c) {
 // once the consumers finished every item of the chunk it held (cons[s]).
 // The producer never waits on a slot while one of its own issued chunks is
 // unpublished, so it cannot hold back a chunk the consumers are waiting for.
-template <class IssueFn, class ItemsFn, class TraceFn>
+template <class IssueFn, class ItemsFn>
 __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, uint32_t S,
-                               uint32_t &issued, IssueFn issue, ItemsFn items, TraceFn trace) {
+                               uint32_t &issued, IssueFn issue, ItemsFn items) {
     uint32_t next = p, pub = p;    // next chunk to issue / to publish
     // Slot c % S is free for chunk c once chunk c - S (its previous user,
     // possibly another producer's) was issued there and fully consumed.  The
@@ -445,7 +445,6 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
         if (pub < next) {
             wait_vm(issued - ends[(pub / kProd) % kMaxS]);
             lds_st(&y->landed[p], pub / kProd + 1);
-            trace(pub);
             pub += kProd;
         } else {
             __builtin_amdgcn_s_sleep(1);   // every own chunk published; wait for a slot
@@ -466,85 +465,45 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
 //      S slots, slot = gate rows[ch] then up rows[ch].
 //
 // Block `bid` of `nblk` takes pairs [PT*bid/nblk, PT*(bid+1)/nblk).
-template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, uint8_t *smem,
-                                                              uint32_t bid, uint32_t nblk,
-                                                              uint32_t ch, uint32_t S) {
-    Q4MI_TR_DECL(bid);
-    Q4MI_TR(31, 0, threadIdx.x == 0);
-    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
-    uint32_t *stab = (uint32_t *)smem;
-    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
-    Sync *Y = (Sync *)(P + 1);
-    int8_t *xq = (int8_t *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));
-    float *xd = (float *)(xq + NT * a.K);
-    uint8_t *ring = smem + al16((size_t)((uint8_t *)(xd + NT * (a.K / 32)) - smem));
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t nt = a.src.n_tok, K = a.K, n_ff = a.n_ff, rb = a.rb_gu;
-    const uint32_t slot_bytes = 2u * ch * rb;
-    const KArgs ka = kargs();
-    const bool uniq = a.src.unique != 0;
-    // the host list's ids, loaded while the block starts up (lane u: id u)
-    const int32_t hid = (uniq && wave < kProd) ? host_ids(ka, a.src.n_fixed) : -1;
-    // consumers issue their prologue loads (codebook entry, first x quad)
-    // as their wave starts, ahead of the weight stream the producers begin
-    // after the barrier
-    const uint32_t nq = nt * K / 4;
-    uint32_t code = 0u;
-    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (wave >= kProd) {
-        const uint32_t c0 = tid - kProd * 64;
-        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
-        if (c0 < nq) v0 = ((const float4 *)a.x)[c0];
-    }
-    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) build_plan(P, a.src, tid);
-    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
-    if (!uniq && bid == 0 && wave == kProd) {   // the down launch reuses this plan
-        for (uint32_t i = lane; i < sizeof(Plan) / 16; i += 64)
-            ((uint4 *)a.gplan)[i] = ((const uint4 *)P)[i];
-    }
-    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
-    const uint32_t PT = nu * n_ff;
-    const uint32_t p0 = (uint32_t)(((uint64_t)PT * bid) / nblk);
-    const uint32_t p1 = (uint32_t)(((uint64_t)PT * (bid + 1)) / nblk);
-    const uint32_t np = p1 - p0;
-    const uint32_t C = (np + ch - 1) / ch;
+__device__ inline uint32_t share_lo(uint32_t PT, uint32_t bid, uint32_t nblk) {
+    return (uint32_t)(((uint64_t)PT * bid) / nblk);
+}
 
-    if (wave < kProd) {
-        const uint8_t *base = a.base;
-        const uint64_t stride = a.stride, og = a.og, ou = a.ou;
-        // every expert id in one register (lane u holds id u): a segment's id
-        // is then one v_readlane, not a memory round trip
-        const int32_t idv = uniq ? hid : (lane < nu ? P->uid[lane] : -1);
-        uint32_t issued = 0;
-        Q4MI_TR(0, 0, tid == 0);
-        auto issue = [&](uint32_t c) {
-            const uint32_t q0 = p0 + c * ch, q1 = min(q0 + ch, p1);
-            uint8_t *sg = ring + (size_t)(c % S) * slot_bytes, *su = sg + (size_t)ch * rb;
-            for (uint32_t q = q0; q < q1;) {   // one expert's run of rows at a time
-                const uint32_t u = q / n_ff, r = q % n_ff;
-                const uint32_t n = min(q1 - q, n_ff - r);
-                const int32_t id = __builtin_amdgcn_readlane(idv, u);
-                const uint8_t *e = base + (uint64_t)id * stride + (uint64_t)r * rb;
-                issued += dma1<UNIT>(sg + (size_t)(q - q0) * rb, e + og, n * rb, lane);
-                issued += dma1<UNIT>(su + (size_t)(q - q0) * rb, e + ou, n * rb, lane);
-                q += n;
-            }
-        };
-        auto items = [&](uint32_t c) { return min(ch, np - c * ch); };
-        produce(Y, P->ends[wave], wave, C, S, issued, issue, items,
-                [&](uint32_t c) { if (c < 12) Q4MI_TR(16 + c, 0, lane == 0); });
-        Q4MI_TR(2, 0, tid == 0);
-        return;
-    }
+// Producer: issue pairs [p0, p1) of the block (gate rows then up rows per
+// chunk).  idv holds expert id u in lane u.
+template <uint32_t UNIT>
+__device__ inline void gu_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *ring, uint32_t ch,
+                                  uint32_t S, int32_t idv, uint32_t p0, uint32_t p1,
+                                  uint32_t wave, uint32_t lane) {
+    const uint8_t *base = a.base;
+    const uint64_t stride = a.stride, og = a.og, ou = a.ou;
+    const uint32_t n_ff = a.n_ff, rb = a.rb_gu, slot_bytes = 2u * ch * rb;
+    const uint32_t np = p1 - p0, C = (np + ch - 1) / ch;
+    uint32_t issued = 0;
+    auto issue = [&](uint32_t c) {
+        const uint32_t q0 = p0 + c * ch, q1 = min(q0 + ch, p1);
+        uint8_t *sg = ring + (size_t)(c % S) * slot_bytes, *su = sg + (size_t)ch * rb;
+        for (uint32_t q = q0; q < q1;) {   // one expert's run of rows at a time
+            const uint32_t u = q / n_ff, r = q % n_ff;
+            const uint32_t n = min(q1 - q, n_ff - r);
+            const int32_t id = __builtin_amdgcn_readlane(idv, u);
+            const uint8_t *e = base + (uint64_t)id * stride + (uint64_t)r * rb;
+            issued += dma1<UNIT>(sg + (size_t)(q - q0) * rb, e + og, n * rb, lane);
+            issued += dma1<UNIT>(su + (size_t)(q - q0) * rb, e + ou, n * rb, lane);
+            q += n;
+        }
+    };
+    auto items = [&](uint32_t c) { return min(ch, np - c * ch); };
+    produce(Y, P->ends[wave], wave, C, S, issued, issue, items);
+}
 
-    // ---- consumers
-    const uint32_t ct = tid - kProd * 64;
-    const uint32_t cw = wave - kProd;               // consumer wave
+// Consumer prologue: q8 of x (v0 = quad ct, loaded by the caller), then
+// wait until every consumer wave finished the shared tables.
+template <int NT>
+__device__ inline void gu_quant_x(const MoeArgs &a, Sync *Y, int8_t *xq, float *xd, float4 v0,
+                                  uint32_t ct, uint32_t lane) {
+    const uint32_t nq = a.src.n_tok * a.K / 4;
     const float4 *xg = (const float4 *)a.x;
-    if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, xq, xd);
     // further quads (several tokens) four loads in flight at a time
     for (uint32_t i0 = ct + kCons; i0 < nq; i0 += 4 * kCons) {
@@ -560,7 +519,16 @@ __device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, 
     }
     if (lane == 0) atomicAdd(&Y->ready, 1u);
     spin_ge(&Y->ready, kConsW);                     // table and q8(x) complete
-    Q4MI_TR(4, 0, ct == 0);
+}
+
+// Consumers: h[u][t][r] of pairs [p0, p0 + np) as their chunks land.
+template <uint32_t TY, int NT, int TPR, int GPT>
+__device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const Plan *P, Sync *Y,
+                                  const int8_t *xq, const float *xd, const uint8_t *ring,
+                                  uint32_t ch, uint32_t S, uint32_t p0, uint32_t np, bool uniq,
+                                  uint32_t ct, uint32_t cw) {
+    const uint32_t nt = a.src.n_tok, K = a.K, n_ff = a.n_ff, rb = a.rb_gu;
+    const uint32_t slot_bytes = 2u * ch * rb;
     constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
     const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
     XRegs<NT, GPT> xr;
@@ -569,7 +537,6 @@ __device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, 
     for (uint32_t b = cw * kTpw; b < np; b += kTeams) {   // b: this wave's first pair
         const uint32_t bl = min(b + kTpw, np) - 1;
         for (uint32_t c = b / ch; c <= bl / ch; c++) wait_chunk(Y, c);
-        if (b / kTeams < 4) Q4MI_TR(5 + 2 * (b / kTeams), 0, ct == 0);
         const uint32_t i = b + sub;
         if (i < np) {
             const uint32_t c = i / ch, j = i % ch;
@@ -609,15 +576,66 @@ __device__ __attribute__((always_inline)) inline void gu_body(const MoeArgs &a, 
             }
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);   // rows of pair i read
         }
-        if (b / kTeams < 4) Q4MI_TR(6 + 2 * (b / kTeams), 0, ct == 0);
     }
-    Q4MI_TR(30, 0, ct == 0);
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
 __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    gu_body<TY, NT, TPR, GPT, UNIT>(a, smem, blockIdx.x, gridDim.x, a.chunk, a.slots);
+    const uint32_t bid = blockIdx.x, nblk = gridDim.x, ch = a.chunk, S = a.slots;
+    Q4MI_TR_DECL(bid);
+    Q4MI_TR(31, 0, threadIdx.x == 0);
+    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
+    uint32_t *stab = (uint32_t *)smem;
+    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
+    Sync *Y = (Sync *)(P + 1);
+    int8_t *xq = (int8_t *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));
+    float *xd = (float *)(xq + NT * a.K);
+    uint8_t *ring = smem + al16((size_t)((uint8_t *)(xd + NT * (a.K / 32)) - smem));
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const KArgs ka = kargs();
+    const bool uniq = a.src.unique != 0;
+    // the host list's ids, loaded while the block starts up (lane u: id u)
+    const int32_t hid = (uniq && wave < kProd) ? host_ids(ka, a.src.n_fixed) : -1;
+    // consumers issue their prologue loads (codebook entry, first x quad)
+    // as their wave starts, ahead of the weight stream the producers begin
+    // after the barrier
+    const uint32_t nq = a.src.n_tok * a.K / 4;
+    uint32_t code = 0u;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (wave >= kProd) {
+        const uint32_t c0 = tid - kProd * 64;
+        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
+        if (c0 < nq) v0 = ((const float4 *)a.x)[c0];
+    }
+    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
+    if (!uniq && tid < 64) build_plan(P, a.src, tid);
+    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    if (!uniq && bid == 0 && wave == kProd) {   // the down launch reuses this plan
+        for (uint32_t i = lane; i < sizeof(Plan) / 16; i += 64)
+            ((uint4 *)a.gplan)[i] = ((const uint4 *)P)[i];
+    }
+    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
+    const uint32_t PT = nu * a.n_ff;
+    const uint32_t p0 = share_lo(PT, bid, nblk), p1 = share_lo(PT, bid + 1, nblk);
+
+    if (wave < kProd) {
+        // every expert id in one register (lane u holds id u): a segment's id
+        // is then one v_readlane, not a memory round trip
+        const int32_t idv = uniq ? hid : (lane < nu ? P->uid[lane] : -1);
+        Q4MI_TR(0, 0, tid == 0);
+        gu_produce<UNIT>(a, P, Y, ring, ch, S, idv, p0, p1, wave, lane);
+        Q4MI_TR(2, 0, tid == 0);
+        return;
+    }
+    const uint32_t ct = tid - kProd * 64;
+    if (kIq) build_stab(stab, code, ct);
+    gu_quant_x<NT>(a, Y, xq, xd, v0, ct, lane);
+    Q4MI_TR(4, 0, ct == 0);
+    gu_compute<TY, NT, TPR, GPT>(a, stab, P, Y, xq, xd, ring, ch, S, p0, p1 - p0, uniq, ct,
+                                 wave - kProd);
+    Q4MI_TR(30, 0, ct == 0);
 }
 
 // ---------------------------------------------------------------- down
@@ -629,118 +647,58 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
 //      hd [nsel_cap][n_ff/32] | ring of S slots, slot = ch experts x kDnRows
 //      rows.
 //
-// Block `bid` owns output rows 8*bid..
-template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
-__device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, uint8_t *smem,
-                                                              uint32_t bid, uint32_t ch,
-                                                              uint32_t S) {
-    Q4MI_TR_DECL(bid);
-    Q4MI_TR(31, 1, threadIdx.x == 0);
-    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
-    uint32_t *stab = (uint32_t *)smem;
-    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
-    Sync *Y = (Sync *)(P + 1);
-    float *part = (float *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));   // [kMaxU][NT][kDnRows]
-    int8_t *hq = (int8_t *)(part + kMaxU * NT * kDnRows);
-    const uint32_t n_ff = a.n_ff, cap = a.nsel_cap;
-    float *hd = (float *)(hq + (size_t)cap * n_ff);
-    uint8_t *ring = smem + al16((size_t)((uint8_t *)(hd + (size_t)cap * (n_ff / 32)) - smem));
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t nt = a.src.n_tok, rb = a.rb_dn;
-    const uint32_t r0 = bid * kDnRows;
-    const uint32_t nr = min(kDnRows, a.n_embd - r0);
-    const uint32_t slot_bytes = ch * kDnRows * rb;
-    const KArgs ka = kargs();
-    const bool uniq = a.src.unique != 0;
-    // the host list's ids (producers) or weights (consumers), loaded while
-    // the block starts up (lane u: entry u)
-    const int32_t hword = !uniq ? 0 : wave < kProd ? host_ids(ka, a.src.n_fixed)
-                                                  : __builtin_bit_cast(int32_t, host_weights(ka, a.src.n_fixed));
-    // consumers issue their prologue loads (codebook entry, y, and for a
-    // host list the first h quads) as their wave starts, ahead of the weight
-    // stream the producers begin after the barrier
-    const uint32_t qpr = n_ff / 4;
-    uint32_t code = 0u;
-    float yv = 0.f;
-    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-    if (wave >= kProd) {
-        const uint32_t c0 = tid - kProd * 64;
-        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
-        // (output o = (t, rr) is summed by the 8 lanes 8o..8o+7; the last
-        // one adds the old y and stores)
-        if ((c0 & 7u) == 7u && (c0 >> 3) < nt * nr) {
-            const uint32_t o = c0 >> 3;
-            yv = a.y[(size_t)(o / nr) * a.n_embd + r0 + o % nr];
-        }
-        if (uniq) {   // pair slot s = h row s * kMaxT
-            const uint32_t nq0 = a.src.n_fixed * qpr;
-            auto hq0 = [&](uint32_t i) {
-                return ((const float4 *)(a.h + (size_t)(i / qpr) * kMaxT * n_ff))[i % qpr];
-            };
-            if (c0 < nq0) v0 = hq0(c0);
-            if (c0 + kCons < nq0) v1 = hq0(c0 + kCons);
-        }
-    }
-    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) {
-        if (a.plan_in) {   // the plan the gate/up launch of this call published
-            for (uint32_t i = tid; i < sizeof(Plan) / 16; i += 64)
-                ((uint4 *)P)[i] = ((const uint4 *)a.gplan)[i];
-        } else {
-            build_plan(P, a.src, tid);
-        }
-    }
-    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
-    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
-    const uint32_t nsel = uniq ? nu : P->nsel;
+// Block `bid` owns output rows 8*bid..8*bid+7.
+template <uint32_t UNIT>
+__device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *ring, uint32_t ch,
+                                  uint32_t S, int32_t idv, uint32_t nu, uint32_t r0, uint32_t nr,
+                                  uint32_t wave, uint32_t lane) {
+    const uint8_t *base = a.base;
+    const uint64_t stride = a.stride, od = a.od;
+    const uint32_t rb = a.rb_dn, slot_bytes = ch * kDnRows * rb;
     const uint32_t C = (nu + ch - 1) / ch;
+    uint32_t issued = 0;
+    auto issue = [&](uint32_t c) {
+        const uint32_t e0 = c * ch, e1 = min(e0 + ch, nu);
+        uint8_t *dst = ring + (size_t)(c % S) * slot_bytes;
+        for (uint32_t u = e0; u < e1; u++) {
+            const int32_t id = __builtin_amdgcn_readlane(idv, u);
+            const uint8_t *e = base + (uint64_t)id * stride + od + (uint64_t)r0 * rb;
+            issued += dma1<UNIT>(dst + (size_t)(u - e0) * nr * rb, e, nr * rb, lane);
+        }
+    };
+    auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
+    produce(Y, P->ends[wave], wave, C, S, issued, issue, items);
+}
+
+// Consumers: q8 of every selected h row, the (expert, row) dots as their
+// chunks land, then y[t][r0 + rr] = yv + sum_u w[u][t] * part[u][t][rr].
+// With `pre`, quads ct and ct + kCons of the host list's h rows are already
+// in v0, v1; yv is the old y of output ct / 8 (lanes with ct % 8 == 7).
+template <uint32_t TY, int NT, int TPR, int GPT>
+__device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *P, Sync *Y,
+                                  float *part, int8_t *hq, float *hd, const uint8_t *ring,
+                                  uint32_t ch, uint32_t S, uint32_t r0, uint32_t nr, uint32_t nu,
+                                  uint32_t nsel, bool uniq, float wv, float yv, float4 v0,
+                                  float4 v1, bool pre, uint32_t ct, uint32_t cw, uint32_t lane) {
+    const uint32_t n_ff = a.n_ff, rb = a.rb_dn, nt = a.src.n_tok;
+    const uint32_t slot_bytes = ch * kDnRows * rb;
     const float *hg = a.h;
-
-    if (wave < kProd) {
-        const uint8_t *base = a.base;
-        const uint64_t stride = a.stride, od = a.od;
-        const int32_t idv = uniq ? hword : (lane < nu ? P->uid[lane] : -1);
-        uint32_t issued = 0;
-        Q4MI_TR(0, 1, tid == 0);
-        auto issue = [&](uint32_t c) {
-            const uint32_t e0 = c * ch, e1 = min(e0 + ch, nu);
-            uint8_t *dst = ring + (size_t)(c % S) * slot_bytes;
-            for (uint32_t u = e0; u < e1; u++) {
-                const int32_t id = __builtin_amdgcn_readlane(idv, u);
-                const uint8_t *e = base + (uint64_t)id * stride + od + (uint64_t)r0 * rb;
-                issued += dma1<UNIT>(dst + (size_t)(u - e0) * nr * rb, e, nr * rb, lane);
-            }
-        };
-        auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
-        produce(Y, P->ends[wave], wave, C, S, issued, issue, items,
-                [&](uint32_t c) { if (c < 12) Q4MI_TR(16 + c, 1, lane == 0); });
-        Q4MI_TR(2, 1, tid == 0);
-        return;
-    }
-
-    // ---- consumers
-    const uint32_t ct = tid - kProd * 64;
-    const uint32_t cw = wave - kProd;
-    // y of this block's rows and the host list's weights (needed at the end;
-    // loaded now, weight u in lane u)
-    const float wv = __builtin_bit_cast(float, hword);
+    const uint32_t qpr = n_ff / 4;
     // host list: its weights go to Plan::w[0] for the final sum
     if (uniq && cw == 0 && lane < nu) P->w[0][lane] = wv;
     // q8 of every selected h row; pair slot s holds h[u][t] (slots of u are
     // its selected tokens in order).  Every prologue load is issued before
     // any is used.
     const uint32_t nq = nsel * qpr;
-    auto hquad = [&](uint32_t i) -> const float4 * {
+    auto hquad = [&](uint32_t i) -> float4 {
         const uint32_t s = i / qpr;
         const uint32_t row = uniq ? s * kMaxT : P->prow[s];
-        return (const float4 *)(hg + (size_t)row * n_ff) + i % qpr;
+        return ((const float4 *)(hg + (size_t)row * n_ff))[i % qpr];
     };
-    if (!uniq) {    // device list: the rows come from the plan
-        if (ct < nq) v0 = *hquad(ct);
-        if (ct + kCons < nq) v1 = *hquad(ct + kCons);
+    if (!pre) {
+        if (ct < nq) v0 = hquad(ct);
+        if (ct + kCons < nq) v1 = hquad(ct + kCons);
     }
-    if (kIq) build_stab(stab, code, ct);
     if (ct < nq) quant_quad(v0, ct, hq, hd);
     if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
     // further quads (many pairs) eight loads in flight at a time
@@ -749,7 +707,7 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t i = i0 + k * kCons;
-            v[k] = i < nq ? *hquad(i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[k] = i < nq ? hquad(i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int k = 0; k < 8; k++)
@@ -757,7 +715,6 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
     }
     if (lane == 0) atomicAdd(&Y->ready, 1u);
     spin_ge(&Y->ready, kConsW);                     // table and q8(h) complete
-    Q4MI_TR(4, 1, ct == 0);
     constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
     const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
     const uint32_t ni = nu * nr;                    // items, expert-major
@@ -765,7 +722,6 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
     for (uint32_t b = cw * kTpw; b < ni; b += kTeams) {
         const uint32_t bl = min(b + kTpw, ni) - 1;
         for (uint32_t c = b / ipc; c <= bl / ipc; c++) wait_chunk(Y, c);
-        if (b / kTeams < 4) Q4MI_TR(5 + 2 * (b / kTeams), 1, ct == 0);
         const uint32_t it = b + sub;
         if (it < ni) {
             const uint32_t c = it / ipc, jj = it % ipc;
@@ -810,11 +766,9 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
             }
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);
         }
-        if (b / kTeams < 4) Q4MI_TR(6 + 2 * (b / kTeams), 1, ct == 0);
     }
     if (lane == 0) atomicAdd(&Y->fin, 1u);
     spin_ge(&Y->fin, kConsW);                       // every partial sum written
-    Q4MI_TR(29, 1, ct == 0);
     // y[t][r] += sum_u w[u][t] * part[u][t][r]: lane sl of an output's
     // 8 lanes takes experts u = sl, sl + 8, ... in plan order, then a fixed
     // DPP tree joins the 8 partial sums (deterministic)
@@ -828,16 +782,95 @@ __device__ __attribute__((always_inline)) inline void dn_body(const MoeArgs &a, 
         const float y0 = c8 == ct ? yv : a.y[(size_t)t * a.n_embd + r0 + rr];
         if (sl == 7u) a.y[(size_t)t * a.n_embd + r0 + rr] = y0 + s;
     }
-    Q4MI_TR(30, 1, ct == 0);
+}
+
+// The old y of output o = ct / 8 (t = o / nr, row r0 + o % nr) in the lane
+// that stores it (ct % 8 == 7), loaded early.
+__device__ inline float dn_y_early(const MoeArgs &a, uint32_t c0, uint32_t r0, uint32_t nr) {
+    if ((c0 & 7u) == 7u && (c0 >> 3) < a.src.n_tok * nr) {
+        const uint32_t o = c0 >> 3;
+        return a.y[(size_t)(o / nr) * a.n_embd + r0 + o % nr];
+    }
+    return 0.f;
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
 __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    dn_body<TY, NT, TPR, GPT, UNIT>(a, smem, blockIdx.x, a.chunk, a.slots);
+    const uint32_t bid = blockIdx.x, ch = a.chunk, S = a.slots;
+    Q4MI_TR_DECL(bid);
+    Q4MI_TR(31, 1, threadIdx.x == 0);
+    constexpr bool kIq = TY == Q4MI_T_IQ3_S;
+    uint32_t *stab = (uint32_t *)smem;
+    Plan *P = (Plan *)(smem + (kIq ? 32768 : 0));
+    Sync *Y = (Sync *)(P + 1);
+    float *part = (float *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));   // [kMaxU][NT][kDnRows]
+    int8_t *hq = (int8_t *)(part + kMaxU * NT * kDnRows);
+    const uint32_t n_ff = a.n_ff, cap = a.nsel_cap;
+    float *hd = (float *)(hq + (size_t)cap * n_ff);
+    uint8_t *ring = smem + al16((size_t)((uint8_t *)(hd + (size_t)cap * (n_ff / 32)) - smem));
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t r0 = bid * kDnRows;
+    const uint32_t nr = min(kDnRows, a.n_embd - r0);
+    const KArgs ka = kargs();
+    const bool uniq = a.src.unique != 0;
+    // the host list's ids (producers) or weights (consumers), loaded while
+    // the block starts up (lane u: entry u)
+    const int32_t hword = !uniq ? 0 : wave < kProd ? host_ids(ka, a.src.n_fixed)
+                                                  : __builtin_bit_cast(int32_t, host_weights(ka, a.src.n_fixed));
+    // consumers issue their prologue loads (codebook entry, y, and for a
+    // host list the first h quads) as their wave starts, ahead of the weight
+    // stream the producers begin after the barrier
+    const uint32_t qpr = n_ff / 4;
+    uint32_t code = 0u;
+    float yv = 0.f;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (wave >= kProd) {
+        const uint32_t c0 = tid - kProd * 64;
+        if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
+        yv = dn_y_early(a, c0, r0, nr);
+        if (uniq) {   // pair slot s = h row s * kMaxT
+            const uint32_t nq0 = a.src.n_fixed * qpr;
+            auto hq0 = [&](uint32_t i) {
+                return ((const float4 *)(a.h + (size_t)(i / qpr) * kMaxT * n_ff))[i % qpr];
+            };
+            if (c0 < nq0) v0 = hq0(c0);
+            if (c0 + kCons < nq0) v1 = hq0(c0 + kCons);
+        }
+    }
+    if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
+    if (!uniq && tid < 64) {
+        if (a.plan_in) {   // the plan the gate/up launch of this call published
+            for (uint32_t i = tid; i < sizeof(Plan) / 16; i += 64)
+                ((uint4 *)P)[i] = ((const uint4 *)a.gplan)[i];
+        } else {
+            build_plan(P, a.src, tid);
+        }
+    }
+    __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
+    const uint32_t nsel = uniq ? nu : P->nsel;
+
+    if (wave < kProd) {
+        const int32_t idv = uniq ? hword : (lane < nu ? P->uid[lane] : -1);
+        Q4MI_TR(0, 1, tid == 0);
+        dn_produce<UNIT>(a, P, Y, ring, ch, S, idv, nu, r0, nr, wave, lane);
+        Q4MI_TR(2, 1, tid == 0);
+        return;
+    }
+    const uint32_t ct = tid - kProd * 64;
+    if (kIq) build_stab(stab, code, ct);
+    dn_compute<TY, NT, TPR, GPT>(a, stab, P, Y, part, hq, hd, ring, ch, S, r0, nr, nu, nsel, uniq,
+                                 __builtin_bit_cast(float, hword), yv, v0, v1, uniq, ct,
+                                 wave - kProd, lane);
+    Q4MI_TR(30, 1, ct == 0);
 }
 
 // ------------------------------------------------------------------ host
+// Measurement hook: bit 0 runs the gate/up launch, bit 1 the down launch
+// (default both).  Lets a benchmark time each kernel of the pair alone.
+static int g_phases = 3;
 constexpr size_t kLdsCap = 160 * 1024;
 
 // LDS budget of a decode block (q4mi_moe_lds_cap lowers it for tests).
@@ -991,18 +1024,6 @@ static bool dn_dispatch(const MoeArgs &a, uint32_t nu_host) {
     return false;
 }
 
-// Measurement hook: bit 0 runs the gate/up launch, bit 1 the down launch
-// (default both).  Lets a benchmark time each kernel of the pair alone.
-static int g_phases = 3;
-
-#ifdef Q4MI_TRACE
-static unsigned long long *g_trace = nullptr;
-extern "C" int q4mi_trace_read(void *dst, int kern) {
-    if (!g_trace || hipDeviceSynchronize() != hipSuccess) return 0;
-    return hipMemcpy(dst, g_trace + (size_t)kern * 4096 * 32, 4096 * 32 * 8,
-                     hipMemcpyDeviceToHost) == hipSuccess;
-}
-#endif
 
 template <int NT>
 static bool run_nt(uint32_t ty_gu, uint32_t ty_dn, const MoeArgs &a, uint32_t nu_host) {
