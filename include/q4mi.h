@@ -30,7 +30,10 @@ extern "C" {
  * src/q4_rocm.cu:852). */
 void *q4_hip_stream(void);
 /* Select the launch stream (hipStream_t; NULL = the default stream).  No
- * reference counterpart: the reference owned one global stream. */
+ * reference counterpart: the reference owned one global stream.  The
+ * library's scratch (fp32 h, the device-list plan, the staged list, the MMQ
+ * buffers) exists once per process, so calls must stay ordered on this one
+ * stream: calls from several host threads or streams at once race. */
 void q4mi_set_stream(void *stream);
 /* Text of the last rejection or launch failure. */
 const char *q4mi_last_error(void);
