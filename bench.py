@@ -243,7 +243,10 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.no_prefill:
+        out["mfma_peak"] = bench_mfma_peak(L, torch, q4mi)
         out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
+        out["prefill"]["pct_of_measured_int8_peak"] = round(
+            100 * out["prefill"]["mmq_TOPS"] / out["mfma_peak"]["int8_TOPS"], 2)
     if not args.no_extra:
         out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1)
         out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
@@ -253,6 +256,29 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
+
+
+def bench_mfma_peak(L, torch, q4mi, iters=16384, reps=5):
+    """Measured dense MFMA rate of this GPU (the int8 32x32x32 and fp16
+    32x32x16 instructions the datasheet peaks are quoted for), from the
+    library's throughput probe timed with events on the library stream."""
+    import ctypes
+    res = {}
+    for kind, key in ((0, "int8_TOPS"), (1, "fp16_TFLOPS")):
+        ops = ctypes.c_uint64(0)
+        q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe")
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        res[key] = round(ops.value / t / 1e12, 1)
+    res["datasheet_int8_TOPS"] = 5000.0
+    res["datasheet_fp16_TFLOPS"] = 2500.0
+    return res
 
 
 PF_T, PF_K = 2048, 10

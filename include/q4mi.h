@@ -82,6 +82,10 @@ void q4mi_moe_phases(int mask);
 /* Test hook: cap the decode kernels' LDS at `bytes` (0: all of it), so their
  * LDS rings get reused within a launch.  No reference counterpart. */
 void q4mi_moe_lds_cap(uint32_t bytes);
+/* Measurement hook (no reference counterpart): one launch of an MFMA
+ * throughput probe on the library stream (kind 0: int8 32x32x32, 1: fp16
+ * 32x32x16); *ops = the launch's ops, for a caller-timed rate. */
+bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops);
 /* One token; slots/wts are HOST arrays of n <= 64 experts.
  * d_y[r] += sum_e wts[e] * down_e(q8(silu(gate_e.q8(x)) * up_e.q8(x))).
  * gt == ut; IQ3_S or Q8_0; in_dim == n_embd.  d_h, d_h2, d_down are

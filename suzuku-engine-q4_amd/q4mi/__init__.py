@@ -46,6 +46,7 @@ _SIGS = {
     "q4_hip_moe_scratch_warm": (None, []),
     "q4mi_moe_phases": (None, [_c.c_int]),
     "q4mi_moe_lds_cap": (None, [_u32]),
+    "q4mi_mfma_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
     "q4_hip_moe_exec": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32, _u64,
                              _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_exec_dev": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u64, _u32, _u64, _u32, _u64,
