@@ -85,7 +85,7 @@ struct __align__(16) Plan {
 
 // Device lists: wave 0 builds the plan (first-appearance order over
 // (token, pick)); callers sync afterwards.
-__device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
+__device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *ht) {
     // lane -> (token, pick) of the flattened lists, token-major
     // every token's count in one load (lane t holds token t's), then
     // read back lane by lane: one memory round trip, not one per token
@@ -111,14 +111,29 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane) {
         w = s.ew[(size_t)tok * s.stride + rem];
     }
     const bool valid = lane < E && id >= 0;
-    // first occurrence of each id: lane reads (v_readlane, a few cycles)
-    // instead of lane shuffles (an LDS round trip each)
+    // First occurrence of each id, through a 1024-bucket table in LDS (ht,
+    // 4 KB of the not-yet-used ring): every valid lane takes the minimum
+    // lane of its bucket; that lane holds the first occurrence of the id
+    // unless it holds another id of the same bucket (ids 1024 apart), which
+    // only the exact pass over the lanes (v_readlane per lane) settles.
     const uint64_t vmask = __ballot(valid);
-    uint32_t first_j = lane;
-    for (uint32_t j = 0; j < E; j++) {
-        if (!((vmask >> j) & 1ull)) continue;
-        const int32_t idj = __builtin_amdgcn_readlane(id, j);
-        if (idj == id && j < first_j) first_j = j;
+    const uint32_t hb = (uint32_t)id & 1023u;
+    if (valid) ht[hb] = 0xFFFFFFFFu;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    if (valid) atomicMin(&ht[hb], lane);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    const uint32_t mlane = valid ? ht[hb] : lane;
+    const bool clash = valid && __shfl(id, (int)mlane) != id;
+    uint32_t first_j = (valid && !clash) ? mlane : lane;
+    if (__ballot(clash)) {
+        first_j = lane;
+        for (uint32_t j = 0; j < E; j++) {
+            if (!((vmask >> j) & 1ull)) continue;
+            const int32_t idj = __builtin_amdgcn_readlane(id, j);
+            if (idj == id && j < first_j) first_j = j;
+        }
     }
     const bool first = valid && first_j == lane;
     const uint64_t fm = __ballot(first);
@@ -610,7 +625,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
         if (c0 < nq) v0 = ((const float4 *)a.x)[c0];
     }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) build_plan(P, a.src, tid);
+    if (!uniq && tid < 64) build_plan(P, a.src, tid, (uint32_t *)ring);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
     if (!uniq && bid == 0 && wave == kProd) {   // the down launch reuses this plan
         for (uint32_t i = lane; i < sizeof(Plan) / 16; i += 64)
@@ -845,7 +860,7 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
             for (uint32_t i = tid; i < sizeof(Plan) / 16; i += 64)
                 ((uint4 *)P)[i] = ((const uint4 *)a.gplan)[i];
         } else {
-            build_plan(P, a.src, tid);
+            build_plan(P, a.src, tid, (uint32_t *)ring);
         }
     }
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -877,6 +892,9 @@ constexpr size_t kLdsCap = 160 * 1024;
 static size_t g_lds_cap = 0;
 static size_t lds_cap() { return g_lds_cap ? std::min(g_lds_cap, kLdsCap) : kLdsCap; }
 
+// bytes of the bucket table build_plan keeps at the start of the ring
+constexpr size_t kPlanTable = 4096;
+
 static size_t head_bytes(uint32_t ty) {
     return al16((ty == Q4MI_T_IQ3_S ? 32768 : 0) + sizeof(Plan) + sizeof(Sync));
 }
@@ -904,7 +922,8 @@ static size_t gu_plan(const MoeArgs &a, uint32_t nu_host, uint32_t grid, size_t 
     const uint32_t C = (share + ch - 1) / ch;
     if (S < 3 && S < C) return 0;
     S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
-    return fixed + (size_t)S * 2 * ch * a.rb_gu;
+    // the ring's first 4 KB hold the device-list plan's bucket table first
+    return std::max(fixed + (size_t)S * 2 * ch * a.rb_gu, fixed + kPlanTable);
 }
 
 // Same for the down kernel (sets a.nsel_cap).
@@ -927,7 +946,7 @@ static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &
     if (S < 2 && S < C) return 0;
     S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
     a.nsel_cap = cap;
-    return fixed + (size_t)S * ch * kDnRows * a.rb_dn;
+    return std::max(fixed + (size_t)S * ch * kDnRows * a.rb_dn, fixed + kPlanTable);
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>

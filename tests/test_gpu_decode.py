@@ -429,3 +429,45 @@ def test_moe_repeated_ids_and_64_experts(gpu, oracle):
                                            q4mi.ptr(yd), ly.n_ff, ly.n_embd, ly.n_embd),
                    "q4_hip_moe_exec_dev")
         assert rel_err(host(yd), yo) <= TOL, len(ids)
+
+
+def test_device_list_bucket_clash(gpu, oracle):
+    """Device lists whose ids share a bucket of the plan's 1024-bucket
+    first-occurrence table (ids 1024 apart), with repeats, on the window and
+    the one-token device-list paths."""
+    ly = Layer(23, n_exp=1040, n_embd=512, n_ff=512)
+    rng = np.random.default_rng(83)
+    lists = [np.array([3, 1027, 10, 3, 1034], np.int32),
+             np.array([1034, 10, 1027, 7, 1039, 15], np.int32)]
+    n_tok = len(lists)
+    x = rng.standard_normal((n_tok, ly.n_embd)).astype(np.float32)
+    es = np.full((n_tok, 64), -1, np.int32)
+    ew = np.zeros((n_tok, 64), np.float32)
+    nh = np.zeros(n_tok, np.int32)
+    ws = []
+    for t, ids in enumerate(lists):
+        w = rng.random(len(ids)).astype(np.float32)
+        es[t, :len(ids)], ew[t, :len(ids)], nh[t] = ids, w, len(ids)
+        ws.append(w)
+    yo = np.stack([oracle.moe_tokens(ly.n_embd, ly.n_ff, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride,
+                                     x[t:t + 1], lists[t][None], ws[t][None])[0]
+                   for t in range(n_tok)])
+    assert gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, T_IQ3_S, ly.n_embd, ly.n_ff, n_tok)
+    d_es, d_ew, d_nh, dx = dev(es), dev(ew), dev(nh), dev(x)
+    y = dev(np.zeros((n_tok, ly.n_embd), np.float32))
+    q4mi.check(gpu.q4_hip_moe_exec_win(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es),
+                                       q4mi.ptr(d_ew), q4mi.ptr(d_nh), n_tok, T_IQ3_S, ly.og,
+                                       T_IQ3_S, ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx), None,
+                                       q4mi.ptr(y), ly.n_ff, ly.n_embd, ly.n_embd),
+               "q4_hip_moe_exec_win")
+    assert rel_err(host(y), yo) <= TOL
+    for t in range(n_tok):
+        d_es1, d_ew1 = dev(es[t]), dev(ew[t])
+        d_n1 = dev(np.array([nh[t]], np.int32))
+        dx1, y1 = dev(x[t]), dev(np.zeros(ly.n_embd, np.float32))
+        q4mi.check(gpu.q4_hip_moe_exec_dev(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es1),
+                                           q4mi.ptr(d_ew1), q4mi.ptr(d_n1), T_IQ3_S, ly.og,
+                                           T_IQ3_S, ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx1), None,
+                                           None, None, q4mi.ptr(y1), ly.n_ff, ly.n_embd,
+                                           ly.n_embd), "q4_hip_moe_exec_dev")
+        assert rel_err(host(y1), yo[t]) <= TOL, t
