@@ -155,22 +155,24 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *h
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-    // pair slots: exclusive prefix of popcount(sel) over u (lane u)
-    const uint32_t c = lane < nu ? (uint32_t)__popc(P->sel[lane]) : 0u;
-    uint32_t incl = c;
+    // pair slots: pslot[u] = sum over v < u of popcount(sel[v]), counted
+    // per token bit with a ballot and mbcnt (no cross-lane round trips)
+    const uint32_t sl = lane < nu ? P->sel[lane] : 0u;
+    uint32_t below = 0, nsel = 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o);
-        if (lane >= (uint32_t)o) incl += v;
+    for (uint32_t t = 0; t < kMaxT; t++) {
+        const uint64_t b = __ballot((sl >> t) & 1u);
+        below += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                           __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        nsel += (uint32_t)__popcll(b);
     }
     if (lane < nu) {
-        P->pslot[lane] = incl - c;
-        uint32_t k = incl - c;
-        const uint32_t sl = P->sel[lane];
+        P->pslot[lane] = below;
+        uint32_t k = below;
         for (uint32_t t = 0; t < kMaxT; t++)
             if ((sl >> t) & 1u) P->prow[k++] = lane * kMaxT + t;
     }
-    if (lane == 63) P->nsel = incl;
+    if (lane == 0) P->nsel = nsel;
 }
 
 // ------------------------------------------------------------ LDS pipeline
