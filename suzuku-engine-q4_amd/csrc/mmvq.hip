@@ -12,9 +12,13 @@ namespace q4mi {
 bool quant8_launch(const float *x, const int32_t *ids, uint64_t rows, uint32_t cols,
                    int8_t *q, float *d, int32_t *bs);
 
+// xf (optional): fp32 activations [nt][K], quantized by every block into
+// LDS behind its weight tile (the q8 codes and scales of q8_quant_k, bit for
+// bit), so a call needs no separate quantize launch; else xq / xd hold them.
 template <class F, int NT, int TPR, int GPT>
 __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uint32_t rows,
                                               uint32_t K, uint32_t rb, uint32_t R,
+                                              const float *__restrict__ xf,
                                               const int8_t *__restrict__ xq,
                                               const float *__restrict__ xd, uint32_t nt,
                                               float *__restrict__ y, float scale,
@@ -25,13 +29,32 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     const uint32_t tid = threadIdx.x;
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nr = min(R, rows - r0);
+    const uint32_t G = K / 32;
     if (F::kTables) q4mi_iq3s_tables_init(tab, tid, 256);
-    stage_tile(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
+    stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
-    load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
+    // pre-quantized codes: loaded while the tile copy is in flight
+    if (!xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
+    if (xf) {
+        // 8 lanes per 32-value group, 32 groups per pass
+        int8_t *lq = (int8_t *)(tile + ((R * rb + 15u) & ~15u));
+        float *ld = (float *)(lq + (size_t)NT * K);
+        for (uint32_t gid = tid >> 3; gid < nt * G; gid += 32) {
+            const uint32_t t = gid / G, g = gid % G, sub = tid & 7u;
+            const float4 v = *(const float4 *)(xf + (size_t)t * K + 32u * g + 4u * sub);
+            float dd;
+            int bsum;
+            const uint32_t packed = q4mi_quant_team8(v, &dd, &bsum);
+            *(uint32_t *)(lq + (size_t)t * K + 32u * g + 4u * sub) = packed;
+            if (sub == 0) ld[gid] = dd;
+        }
+        xq = lq;
+        xd = ld;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    const uint32_t G = K / 32;
+    if (xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
     for (uint32_t rr = tid / TPR; rr < nr; rr += 256 / TPR) {
         float acc[NT];
 #pragma unroll
@@ -48,20 +71,25 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     }
 }
 
+// weight bytes per row tile
+static uint32_t tile_target(uint32_t ty) { return ty == Q4MI_T_Q8_0 ? 24576u : 14336u; }
+
 template <class F, int NT>
-static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const int8_t *xq,
-                           const float *xd, uint32_t nt, float *y, float scale,
-                           int32_t *sums) {
+static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const float *xf,
+                           const int8_t *xq, const float *xd, uint32_t nt, float *y,
+                           float scale, int32_t *sums) {
     const uint32_t G = K / 32;
     const RowLayout L = layout_for(G);
     const uint32_t rb = (uint32_t)q4mi_row_bytes(F::kType, K);
-    const uint32_t target = F::kType == Q4MI_T_Q8_0 ? 24576u : 14336u;
+    const uint32_t target = tile_target(F::kType);
     const uint32_t R = tile_rows(rb, L.tpr, target);
-    const size_t lds = (F::kTables ? sizeof(Iq3sLds) : 0) + (size_t)R * rb + 64;
+    const size_t xlds = xf ? (size_t)NT * K + (size_t)NT * (K / 32) * 4 : 0;
+    const size_t lds = (F::kTables ? sizeof(Iq3sLds) : 0) + (((size_t)R * rb + 15) & ~(size_t)15) +
+                       xlds + 64;
     const dim3 grid((rows + R - 1) / R), blk(256);
 #define Q4MI_L(T, P)                                                                     \
     if (L.tpr == T && L.gpt == P) {                                                      \
-        mmvq_k<F, NT, T, P><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xq, xd, nt, \
+        mmvq_k<F, NT, T, P><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, xq, xd, nt, \
                                                           y, scale, sums);               \
         return launch_ok("mmvq_k");                                                      \
     }
@@ -72,12 +100,13 @@ static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const in
 }
 
 template <class F>
-static bool mmvq_launch(const uint8_t *W, uint32_t rows, uint32_t K, const int8_t *xq,
-                        const float *xd, uint32_t nt, float *y, float scale, int32_t *sums) {
-    if (nt == 1) return mmvq_launch_nt<F, 1>(W, rows, K, xq, xd, nt, y, scale, sums);
-    if (nt == 2) return mmvq_launch_nt<F, 2>(W, rows, K, xq, xd, nt, y, scale, sums);
-    if (nt <= 4) return mmvq_launch_nt<F, 4>(W, rows, K, xq, xd, nt, y, scale, sums);
-    return mmvq_launch_nt<F, 8>(W, rows, K, xq, xd, nt, y, scale, sums);
+static bool mmvq_launch(const uint8_t *W, uint32_t rows, uint32_t K, const float *xf,
+                        const int8_t *xq, const float *xd, uint32_t nt, float *y, float scale,
+                        int32_t *sums) {
+    if (nt == 1) return mmvq_launch_nt<F, 1>(W, rows, K, xf, xq, xd, nt, y, scale, sums);
+    if (nt == 2) return mmvq_launch_nt<F, 2>(W, rows, K, xf, xq, xd, nt, y, scale, sums);
+    if (nt <= 4) return mmvq_launch_nt<F, 4>(W, rows, K, xf, xq, xd, nt, y, scale, sums);
+    return mmvq_launch_nt<F, 8>(W, rows, K, xf, xq, xd, nt, y, scale, sums);
 }
 
 bool mmvq_covered(uint32_t ty, uint64_t K) {
@@ -89,8 +118,34 @@ bool mmvq_covered(uint32_t ty, uint64_t K) {
 bool mmvq_q8(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const int8_t *xq,
              const float *xd, uint32_t nt, float *y, float scale, int32_t *sums) {
     if (ty == Q4MI_T_IQ3_S)
-        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, xq, xd, nt, y, scale, sums);
-    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, xq, xd, nt, y, scale, sums);
+        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, nullptr, xq, xd, nt, y,
+                                    scale, sums);
+    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, nullptr, xq, xd, nt, y, scale,
+                               sums);
+}
+
+// Activations quantized inside the GEMV blocks: used while the codes of the
+// padded token count fit 16 KB of LDS beside the tile and the call has at
+// most 1024 row tiles.  Every block re-reads and re-quantizes all of x, so
+// a tall matrix (config 4: 18992 tiles) is faster with one quantize launch
+// (measured: 56.5 against 70.8 us at 1 token), a short one (config 0: 512
+// tiles) without it (7.97 against 7.32 us).
+static bool mmvq_fused_fits(uint32_t ty, uint64_t rows, uint64_t K, uint32_t nt) {
+    const uint32_t ntp = nt == 1 ? 1 : nt == 2 ? 2 : nt <= 4 ? 4 : 8;
+    if ((uint64_t)ntp * K > 16384) return false;
+    const RowLayout L = layout_for((uint32_t)(K / 32));
+    const uint32_t rb = (uint32_t)q4mi_row_bytes(ty, K);
+    const uint32_t R = tile_rows(rb, L.tpr, tile_target(ty));
+    return (rows + R - 1) / R <= 1024;
+}
+
+static bool mmvq_f32(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const float *x,
+                     uint32_t nt, float *y, float scale) {
+    if (ty == Q4MI_T_IQ3_S)
+        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, x, nullptr, nullptr, nt, y,
+                                    scale, nullptr);
+    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, x, nullptr, nullptr, nt, y, scale,
+                               nullptr);
 }
 
 static int g_on = -1;
@@ -139,6 +194,11 @@ bool q4_mmvq_n(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
         nrows > 0x7fffffffu || !mmvq_covered(ty, ncols)) {
         set_error("q4_mmvq_n: not covered");
         return false;
+    }
+    if ((uintptr_t)d_x % 16 == 0 && mmvq_fused_fits(ty, nrows, ncols, n)) {
+        // every block quantizes x itself: no quantize launch, no held codes
+        g_cur_x = nullptr;
+        return mmvq_f32(ty, d_w, nrows, ncols, d_x, n, d_y, scale);
     }
     if (!ensure_xq((size_t)8 * 8192)) return false;
     Scratch &s = scratch();

@@ -99,8 +99,6 @@ __device__ inline void row_dot(const Iq3sLds *tab, const uint8_t *lb, const uint
     }
 }
 
-// Copy nbytes (even) from global src to LDS dst with the widest aligned
-// accesses the addresses allow; all threads of the block take part.
 // Wait until at most n VMEM operations of this wave are outstanding.  The
 // count is an instruction immediate, so a runtime n selects among literal
 // waits; n beyond the 6-bit field waits for more than asked, never less.
@@ -182,12 +180,16 @@ __device__ inline void lds_dma16(const void *g, uint32_t lds) {
                  :: "v"(g), "s"(lds) : "memory", "m0");
 }
 
-__device__ inline void stage_tile(uint8_t *dst, const uint8_t *src, uint32_t nbytes,
-                                  uint32_t tid, uint32_t nthr) {
+// Start copying nbytes (even) from global src to LDS dst with the widest
+// aligned accesses the addresses allow; all threads of the block take part.
+// 16-byte-aligned spans go by global -> LDS DMA and stay in flight (the
+// caller waits with vmcnt(0) and a barrier); other spans are copied through
+// registers before this returns (visible after the caller's barrier).
+__device__ inline void stage_tile_issue(uint8_t *dst, const uint8_t *src, uint32_t nbytes,
+                                        uint32_t tid, uint32_t nthr) {
     const uintptr_t a = (uintptr_t)src | nbytes;
     if ((a & 15u) == 0) {
-        // every copy of the block in flight at once (1 KB per wave op), one
-        // wait; the caller's barrier makes the other waves' parts visible
+        // every copy of the block in flight at once (1 KB per wave op)
         const uint32_t lane = tid & 63u, nw = nthr / 64;
         const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
         const uint32_t l0 = (uint32_t)(uintptr_t)dst;   // LDS offset: low half of the flat address
@@ -195,7 +197,6 @@ __device__ inline void stage_tile(uint8_t *dst, const uint8_t *src, uint32_t nby
             const uint32_t off = 1024u * j + 16u * lane;
             if (off < nbytes) lds_dma16(src + off, l0 + 1024u * j);
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else if ((a & 3u) == 0) {
         const uint32_t *s = (const uint32_t *)src;
         uint32_t *d = (uint32_t *)dst;

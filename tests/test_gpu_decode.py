@@ -149,6 +149,33 @@ def test_q4_mmvq_n_abi(gpu, oracle):
     assert not gpu.q4_mmvq_n(99, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y), 1.0, 1)
 
 
+@pytest.mark.parametrize("ty,K,rows,n", [(T_IQ3_S, 4096, 300, 1), (T_IQ3_S, 4096, 97, 3),
+                                         (T_IQ3_S, 8192, 64, 4), (T_Q8_0, 2048, 517, 8),
+                                         (T_Q8_0, 512, 100, 2), (T_IQ3_S, 256, 41, 5)])
+def test_q4_mmvq_n_in_block_quant(gpu, ty, K, rows, n):
+    """q4_mmvq_n quantizes x inside the GEMV blocks when the codes fit beside
+    the tile (else through the quantize launch); both give the pre-quantized
+    entry's results bit for bit, and the hold/release reuse still holds."""
+    import torch
+    rng = np.random.default_rng(K + n)
+    w = synth.matrix(rng, ty, rows, K)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    y_ref, _ = mmvq_gpu(gpu, ty, w, rows, K, x)
+    dw, dx = dev(w), dev(x)
+    y = empty((n, rows), torch.float32)
+    gpu.q4_mmvq_warm()
+    q4mi.check(gpu.q4_mmvq_n(ty, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y), 1.0, n),
+               "q4_mmvq_n")
+    assert np.array_equal(host(y).view(np.uint32), y_ref.view(np.uint32))
+    gpu.q4_mmvq_hold(q4mi.ptr(dx))
+    for _ in range(2):
+        y2 = empty((n, rows), torch.float32)
+        q4mi.check(gpu.q4_mmvq_n(ty, q4mi.ptr(dw), rows, K, q4mi.ptr(dx), q4mi.ptr(y2), 1.0,
+                                 n), "q4_mmvq_n held")
+        assert np.array_equal(host(y2).view(np.uint32), y_ref.view(np.uint32))
+    gpu.q4_mmvq_release()
+
+
 def test_config0_full(gpu, oracle):
     """IQ3_S 4096x4096, one token."""
     rng = np.random.default_rng(0)
