@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
         row_dot<F, NT, GPT, TPR>(tab, tile, (const uint32_t *)tile, rr * rb, gi, x, acc, srow,
                                  (size_t)rows * G);
         reduce_acc<TPR, NT>(acc);
-        if (gi == 0) {
+        if (gi == TPR - 1) {
 #pragma unroll
             for (int t = 0; t < NT; t++)
                 if ((uint32_t)t < nt) y[(size_t)t * rows + r0 + rr] = scale * acc[t];

@@ -8,7 +8,7 @@
 // in registers for every row of the tile.  Per group the lane decodes the
 // weights to signed int8 quads, takes v_dot4_i32_i8 against the activation
 // quads, scales the exact int32 group sum by (2s+1) and accumulates
-// float(S) * (d_w * d_x).  A shuffle reduction over the TPR lanes finishes
+// float(S) * (d_w * d_x).  A DPP reduction over the TPR lanes finishes
 // the row.
 #pragma once
 #include "q4mi_common.h"
@@ -208,10 +208,11 @@ __device__ inline void stage_tile_issue(uint8_t *dst, const uint8_t *src, uint32
     }
 }
 
+// Row totals by a DPP tree: valid in the row's last lane (gi == TPR - 1).
 template <int TPR, int NT>
 __device__ inline void reduce_acc(float (&acc)[NT]) {
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = q4mi_sum_width<TPR>(acc[t]);
+    for (int t = 0; t < NT; t++) acc[t] = q4mi_rsum<TPR>(acc[t]);
 }
 
 // Layout of lanes over a row of G = K/32 groups.

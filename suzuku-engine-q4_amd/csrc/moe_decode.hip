@@ -240,21 +240,6 @@ __device__ inline void quant_quad(float4 v, uint32_t i, int8_t *q, float *d) {
     if ((i & 7u) == 0) d[i / 8] = dd;
 }
 
-// DPP reduction over aligned groups of W lanes (W = 8, 16, 32, 64); the
-// group's total lands in its last lane (lane % W == W-1).
-template <int W>
-__device__ inline float rsum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xF, 0xF, true));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xF, 0xF, true));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
-    if (W >= 16)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xF, 0xF, true));
-    if (W >= 32)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, true));
-    if (W >= 64)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, true));
-    return v;
-}
 
 // Signed int8 quads of IQ3_S group g of the row at LDS offset `row`.
 __device__ inline void iq3s_group(const uint32_t *stab, const uint8_t *lb, const uint32_t *lw,
@@ -588,7 +573,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 if (!((sel >> t) & 1u)) continue;
-                const float gs = rsum<TPR>(ag[t]), us = rsum<TPR>(au[t]);
+                const float gs = q4mi_rsum<TPR>(ag[t]), us = q4mi_rsum<TPR>(au[t]);
                 if (gi == TPR - 1) hout[((size_t)u * kMaxT + t) * n_ff + r] = silu_f(gs) * us;
             }
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);   // rows of pair i read
@@ -778,7 +763,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
             }
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                const float v = ((sel >> t) & 1u) ? rsum<TPR>(acc[t]) : 0.f;
+                const float v = ((sel >> t) & 1u) ? q4mi_rsum<TPR>(acc[t]) : 0.f;
                 if (gi == TPR - 1) part[((size_t)u * NT + t) * kDnRows + rr] = v;
             }
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);
@@ -794,7 +779,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
         float s = 0.f;
         for (uint32_t u = sl; u < nu; u += 8)
             if (uniq || ((P->sel[u] >> t) & 1u)) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
-        s = rsum<8>(s);
+        s = q4mi_rsum<8>(s);
         // outputs past the first kCons / 8 read their old y here
         const float y0 = c8 == ct ? yv : a.y[(size_t)t * a.n_embd + r0 + rr];
         if (sl == 7u) a.y[(size_t)t * a.n_embd + r0 + rr] = y0 + s;
