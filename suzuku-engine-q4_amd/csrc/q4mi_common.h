@@ -42,23 +42,38 @@ __device__ inline int q4mi_q8_code(float v) {
     return (int)r;
 }
 
+// Cross-lane step of an 8-lane team as a DPP move (no LDS round trip):
+// 0xB1 = quad_perm(1,0,3,2) (lane ^ 1), 0x4E = quad_perm(2,3,0,1)
+// (lane ^ 2), 0x141 = row_half_mirror (lane 7 - i within the 8: after the
+// two quad steps every lane of a quad holds the same value, so this takes
+// the other quad's).  Max and integer sums over the team are then exact and
+// every lane holds the result.
+template <int CTRL>
+__device__ inline int q4mi_team8_swap(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ inline float q4mi_team8_swap(float v) {
+    return __builtin_bit_cast(float, q4mi_team8_swap<CTRL>(__builtin_bit_cast(int, v)));
+}
+
 // Lane-cooperative quantizer: 8 lanes own one group, 4 consecutive values
 // each (lane sub = lane & 7 holds values 4*sub..4*sub+3).  Returns the packed
 // int8 codes of this lane's 4 values; *d and *bs are valid in every lane of
 // the 8-lane team.
 __device__ inline uint32_t q4mi_quant_team8(float4 v, float *d, int *bs) {
     float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    a = fmaxf(a, __shfl_xor(a, 1, 8));
-    a = fmaxf(a, __shfl_xor(a, 2, 8));
-    a = fmaxf(a, __shfl_xor(a, 4, 8));
+    a = fmaxf(a, q4mi_team8_swap<0xB1>(a));    // lane ^ 1
+    a = fmaxf(a, q4mi_team8_swap<0x4E>(a));    // lane ^ 2
+    a = fmaxf(a, q4mi_team8_swap<0x141>(a));   // the other quad of the team
     *d = __fdiv_rn(a, 127.f);
     const float sc = a > 0.f ? __fdiv_rn(127.f, a) : 0.f;
     const int c0 = q4mi_q8_code(v.x * sc), c1 = q4mi_q8_code(v.y * sc);
     const int c2 = q4mi_q8_code(v.z * sc), c3 = q4mi_q8_code(v.w * sc);
     int s = c0 + c1 + c2 + c3;
-    s += __shfl_xor(s, 1, 8);
-    s += __shfl_xor(s, 2, 8);
-    s += __shfl_xor(s, 4, 8);
+    s += q4mi_team8_swap<0xB1>(s);
+    s += q4mi_team8_swap<0x4E>(s);
+    s += q4mi_team8_swap<0x141>(s);
     *bs = s;
     return (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
            ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
