@@ -20,6 +20,11 @@ __device__ inline uint32_t f2key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// inverse of f2key
+__device__ inline float key2f(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // Wave maximum of an unsigned value (DPP row shifts, then the row
 // broadcasts; the total lands in lane 63), returned to every lane.
 __device__ inline uint32_t wave_max_u32(uint32_t v) {
@@ -55,16 +60,14 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
         v[j] = i < n_exp ? lg[i] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = key2f(wave_max_u32(f2key(mx)));   // DPP tree, no LDS round trips
     float e[8], s = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         e[j] = (lane + 64u * j) < n_exp ? expf(v[j] - mx) : 0.f;
         s += e[j];
     }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+    s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, q4mi_rsum<64>(s)), 63));
     const float inv = s > 0.f ? __fdiv_rn(1.f, s) : 0.f;
     uint32_t alive = 0;
 #pragma unroll
