@@ -444,7 +444,7 @@ def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):
     del ws
     return {"us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
             "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
-            "note": "includes the q8 quantize launch; eager launches"}
+            "note": "fp32 x in, q8 quantization included (inside the GEMV blocks for <= 1024 row tiles, else one quantize launch); eager launches"}
 
 
 if __name__ == "__main__":
