@@ -97,12 +97,10 @@ __global__ __launch_bounds__(1024) void mmq_tiles_k(const int32_t *__restrict__ 
     auto field = [](uint32_t c) { return 16u * c; };
     uint64_t mine = (uint64_t)nfull << field(fcls);
     if (tcls < 4) mine += 1ull << field(tcls);
-    uint64_t incl = mine;
-#pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) {
-        const uint64_t v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
-    }
+    // every field's sums stay below 2^16, so the two 32-bit halves scan
+    // independently (no carry crosses bit 32)
+    const uint64_t incl = (uint64_t)q4mi_wave_incl_scan((uint32_t)mine) |
+                          ((uint64_t)q4mi_wave_incl_scan((uint32_t)(mine >> 32)) << 32);
     if (lane == 63) wsum[w] = incl;
     __syncthreads();
     uint64_t before = 0, total = 0;

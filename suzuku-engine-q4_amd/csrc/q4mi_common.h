@@ -187,4 +187,17 @@ __device__ inline float q4mi_rsum(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave by DPP (row shifts 1, 2,
+// 4, 8 within each 16-lane row, then the row-15 and row-31 broadcasts carry
+// the earlier rows' totals forward).
+__device__ inline uint32_t q4mi_wave_incl_scan(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, true);
+    return v;
+}
+
 #define Q4MI_CHECK_LAUNCH() (hipGetLastError() == hipSuccess)
