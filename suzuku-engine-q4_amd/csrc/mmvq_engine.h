@@ -53,12 +53,13 @@ struct XRegs {
 };
 
 // xq: [nt][K] int8, xd: [nt][K/32] (global or LDS); tokens >= nt read as 0.
-template <int NT, int GPT, int TPR>
+// Lane gi's groups: gi + TPR*m, or with ADJ the adjacent GPT*gi + m.
+template <int NT, int GPT, int TPR, bool ADJ = false>
 __device__ inline void load_xregs(XRegs<NT, GPT> &x, const int8_t *xq, const float *xd,
                                   uint32_t K, uint32_t nt, uint32_t gi) {
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
-        const uint32_t g = gi + TPR * m;
+        const uint32_t g = ADJ ? GPT * gi + m : gi + TPR * m;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if ((uint32_t)t < nt) {

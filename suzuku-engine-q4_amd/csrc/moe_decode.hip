@@ -241,6 +241,25 @@ __device__ inline void quant_quad(float4 v, uint32_t i, int8_t *q, float *d) {
 }
 
 
+// Signed int8 quads of one IQ3_S group from its raw bytes: q0, q1 = the 8
+// qs bytes, qh = its high-bit byte, sg = its 4 sign bytes.
+__device__ inline void iq3s_quads(const uint32_t *stab, uint32_t q0, uint32_t q1, uint32_t qh,
+                                  uint32_t sg, int32_t (&w)[8]) {
+    // byte k of hlo / hhi: (sign nibble << 1 | qh bit) of quad k / k+4
+    const uint32_t ne = sg & 0x0F0F0F0Fu, no = (sg >> 4) & 0x0F0F0F0Fu;
+    const uint32_t slo = __builtin_amdgcn_perm(no, ne, 0x05010400u);
+    const uint32_t shi = __builtin_amdgcn_perm(no, ne, 0x07030602u);
+    const uint32_t blo = __umul24(qh & 15u, 0x00204081u) & 0x01010101u;
+    const uint32_t bhi = __umul24((qh >> 4) & 15u, 0x00204081u) & 0x01010101u;
+    const uint32_t hlo = (slo << 1) | blo, hhi = (shi << 1) | bhi;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t sel = 0x0C0C0000u | ((4u + (k & 3)) << 8) | (uint32_t)(k & 3);
+        const uint32_t idx = __builtin_amdgcn_perm(k < 4 ? hlo : hhi, k < 4 ? q0 : q1, sel);
+        w[k] = (int32_t)stab[idx];
+    }
+}
+
 // Signed int8 quads of IQ3_S group g of the row at LDS offset `row`.
 __device__ inline void iq3s_group(const uint32_t *stab, const uint8_t *lb, const uint32_t *lw,
                                   uint32_t row, uint32_t g, int32_t (&w)[8], int &mult,
@@ -257,19 +276,32 @@ __device__ inline void iq3s_group(const uint32_t *stab, const uint8_t *lb, const
     const uint32_t sg = lds_u32_at(lw, B + 74u + 4u * j);
     const uint32_t sc = lb[B + 106u + (j >> 1)];
     mult = 2 * (int)((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1;
-    // byte k of hlo / hhi: (sign nibble << 1 | qh bit) of quad k / k+4
-    const uint32_t ne = sg & 0x0F0F0F0Fu, no = (sg >> 4) & 0x0F0F0F0Fu;
-    const uint32_t slo = __builtin_amdgcn_perm(no, ne, 0x05010400u);
-    const uint32_t shi = __builtin_amdgcn_perm(no, ne, 0x07030602u);
-    const uint32_t blo = __umul24(qh & 15u, 0x00204081u) & 0x01010101u;
-    const uint32_t bhi = __umul24(qh >> 4, 0x00204081u) & 0x01010101u;
-    const uint32_t hlo = (slo << 1) | blo, hhi = (shi << 1) | bhi;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t sel = 0x0C0C0000u | ((4u + (k & 3)) << 8) | (uint32_t)(k & 3);
-        const uint32_t idx = __builtin_amdgcn_perm(k < 4 ? hlo : hhi, k < 4 ? q0 : q1, sel);
-        w[k] = (int32_t)stab[idx];
-    }
+    iq3s_quads(stab, q0, q1, qh, sg, w);
+}
+
+// Groups g and g + 1 (g even: one superblock, one scale byte) with their
+// shared reads done once: d, the scale byte, both qh bytes in one 16-bit
+// read (B is even), the 16 qs bytes from five dwords.
+__device__ inline void iq3s_group2(const uint32_t *stab, const uint8_t *lb, const uint32_t *lw,
+                                   uint32_t row, uint32_t g, int32_t (&wa)[8], int32_t (&wb)[8],
+                                   int &ma, int &mb, float &d) {
+    const uint32_t B = row + (g >> 3) * IQ3S_BYTES;
+    const uint32_t j = g & 7u;
+    d = q4mi_h2f(lds_u16_at(lb, B));
+    const uint32_t qo = B + 2u + 8u * j;
+    const uint32_t i0 = qo >> 2, sh = qo & 3u;
+    const uint32_t w0 = lw[i0], w1 = lw[i0 + 1], w2 = lw[i0 + 2], w3 = lw[i0 + 3],
+                   w4 = lw[i0 + 4];
+    const uint32_t qh2 = lds_u16_at(lb, B + 66u + j);
+    const uint32_t sga = lds_u32_at(lw, B + 74u + 4u * j);
+    const uint32_t sgb = lds_u32_at(lw, B + 78u + 4u * j);
+    const uint32_t sc = lb[B + 106u + (j >> 1)];
+    ma = 2 * (int)(sc & 15u) + 1;
+    mb = 2 * (int)(sc >> 4) + 1;
+    iq3s_quads(stab, __builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+               qh2 & 0xffu, sga, wa);
+    iq3s_quads(stab, __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh),
+               qh2 >> 8, sgb, wb);
 }
 
 __device__ inline void q80_group(const uint8_t *lb, const uint32_t *lw, uint32_t row, uint32_t g,
@@ -533,8 +565,11 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     const uint32_t slot_bytes = 2u * ch * rb;
     constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
     const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
+    // IQ3_S with an even group count per lane: lane gi takes the adjacent
+    // groups GPT*gi + m, decoded in pairs that share their superblock reads
+    constexpr bool kPair = TY == Q4MI_T_IQ3_S && GPT % 2 == 0;
     XRegs<NT, GPT> xr;
-    load_xregs<NT, GPT, TPR>(xr, xq, xd, K, nt, gi);
+    load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi);
     float *hout = a.h;
     for (uint32_t b = cw * kTpw; b < np; b += kTeams) {   // b: this wave's first pair
         const uint32_t bl = min(b + kTpw, np) - 1;
@@ -549,24 +584,44 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
             float ag[NT], au[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.f;
+            auto dot = [&](int m, int which, const int32_t (&w)[8], int mult, float d)
+                __attribute__((always_inline)) {
 #pragma unroll
-            for (int m = 0; m < GPT; m++) {
-                const uint32_t g = gi + TPR * m;
+                for (int t = 0; t < NT; t++) {
+                    if (!((sel >> t) & 1u)) continue;
+                    int s = 0;
 #pragma unroll
-                for (int which = 0; which < 2; which++) {
-                    int32_t w[8];
-                    int mult;
-                    float d;
-                    group_w<TY>(stab, tile, tw, (which * ch + j) * rb, g, w, mult, d);
+                    for (int k = 0; k < 8; k++) s = q4mi_sdot4(w[k], xr.q[m][t][k], s);
+                    const float f = (float)(s * mult) * (d * xr.d[m][t]);
+                    if (which == 0) ag[t] += f;
+                    else au[t] += f;
+                }
+            };
+            if constexpr (kPair) {
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if (!((sel >> t) & 1u)) continue;
-                        int s = 0;
+                for (int m = 0; m < GPT; m += 2) {
+                    const uint32_t g = GPT * gi + m;
 #pragma unroll
-                        for (int k = 0; k < 8; k++) s = q4mi_sdot4(w[k], xr.q[m][t][k], s);
-                        const float f = (float)(s * mult) * (d * xr.d[m][t]);
-                        if (which == 0) ag[t] += f;
-                        else au[t] += f;
+                    for (int which = 0; which < 2; which++) {
+                        int32_t wa[8], wb[8];
+                        int ma, mb;
+                        float d;
+                        iq3s_group2(stab, tile, tw, (which * ch + j) * rb, g, wa, wb, ma, mb, d);
+                        dot(m, which, wa, ma, d);
+                        dot(m + 1, which, wb, mb, d);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < GPT; m++) {
+                    const uint32_t g = gi + TPR * m;
+#pragma unroll
+                    for (int which = 0; which < 2; which++) {
+                        int32_t w[8];
+                        int mult;
+                        float d;
+                        group_w<TY>(stab, tile, tw, (which * ch + j) * rb, g, w, mult, d);
+                        dot(m, which, w, mult, d);
                     }
                 }
             }
