@@ -790,13 +790,8 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
             float acc[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) acc[t] = 0.f;
-#pragma unroll
-            for (int m = 0; m < GPT; m++) {
-                const uint32_t g = gi + TPR * m;
-                int32_t w[8];
-                int mult;
-                float d;
-                group_w<TY>(stab, tile, tw, jj * rb, g, w, mult, d);
+            auto dot = [&](uint32_t g, const int32_t (&w)[8], int mult, float d)
+                __attribute__((always_inline)) {
                 uint32_t s2 = ps;
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
@@ -814,6 +809,30 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
                     s = q4mi_sdot4(w[7], qb.w, s);
                     acc[t] = fmaf((float)(s * mult), d * hd[(size_t)s2 * (n_ff / 32) + g], acc[t]);
                     s2++;
+                }
+            };
+            // IQ3_S with an even group count per lane: adjacent groups
+            // GPT*gi + m, decoded in pairs sharing their superblock reads
+            if constexpr (TY == Q4MI_T_IQ3_S && GPT % 2 == 0) {
+#pragma unroll
+                for (int m = 0; m < GPT; m += 2) {
+                    const uint32_t g = GPT * gi + m;
+                    int32_t wa[8], wb[8];
+                    int ma, mb;
+                    float d;
+                    iq3s_group2(stab, tile, tw, jj * rb, g, wa, wb, ma, mb, d);
+                    dot(g, wa, ma, d);
+                    dot(g + 1, wb, mb, d);
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < GPT; m++) {
+                    const uint32_t g = gi + TPR * m;
+                    int32_t w[8];
+                    int mult;
+                    float d;
+                    group_w<TY>(stab, tile, tw, jj * rb, g, w, mult, d);
+                    dot(g, w, mult, d);
                 }
             }
 #pragma unroll
