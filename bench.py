@@ -129,9 +129,13 @@ def main():
     from q4mi import synth
 
     L = q4mi.lib()
+    # the measurement build runs one kernel of the decode pair alone
+    M = q4mi.meas()
     torch.cuda.set_device(0)
     q4mi.use_torch_stream()
+    q4mi.use_torch_stream(M)
     L.q4_hip_moe_scratch_warm()
+    M.q4_hip_moe_scratch_warm()
     stride, og, ou, od = synth.expert_stride(N_EMBD, N_FF)
     rng = np.random.default_rng(1234)
     NL = args.layers
@@ -141,13 +145,13 @@ def main():
     rts = routes(rng, NL)
     T = q4mi.T_IQ3_S
 
-    def layer_call(l):
+    def layer_call(l, lib=L):
         ids, w = rts[l]
-        ok = L.q4_hip_moe_exec(arenas[l].data_ptr(), stride, ids.ctypes.data_as(ctypes.c_void_p),
+        ok = lib.q4_hip_moe_exec(arenas[l].data_ptr(), stride, ids.ctypes.data_as(ctypes.c_void_p),
                                w.ctypes.data_as(ctypes.c_void_p), len(ids), T, og, T, ou, T, od,
                                xs[l].data_ptr(), None, None, None, ys[l].data_ptr(), N_FF,
                                N_EMBD, N_EMBD)
-        q4mi.check(ok, "q4_hip_moe_exec")
+        q4mi.check(ok, "q4_hip_moe_exec", lib)
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
@@ -159,13 +163,15 @@ def main():
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
             q4mi.use_torch_stream()
+            q4mi.use_torch_stream(M)
             fn()
         q4mi.use_torch_stream()
+        q4mi.use_torch_stream(M)
         return g
 
-    def stack():
+    def stack(lib=L):
         for l in range(NL):
-            layer_call(l)
+            layer_call(l, lib)
 
     def timed(g, steps, warmup):
         for _ in range(warmup):
@@ -196,13 +202,14 @@ def main():
     value = LAYER_BYTES / t_layer / 1e9
 
     # the gate/up kernel alone (dominant kernel: 2/3 of the bytes)
-    L.q4mi_moe_phases(1)
-    g_gu = capture(stack)
+    # (measurement build; its kernels are the product's, compiled alike)
+    M.q4mi_moe_phases(1)
+    g_gu = capture(lambda: stack(M))
     ms_gu = timed(g_gu, args.steps, args.warmup)
-    L.q4mi_moe_phases(2)
-    g_dn = capture(stack)
+    M.q4mi_moe_phases(2)
+    g_dn = capture(lambda: stack(M))
     ms_dn = timed(g_dn, args.steps, args.warmup)
-    L.q4mi_moe_phases(3)
+    M.q4mi_moe_phases(3)
     t_gu = ms_gu * 1e-3 / (args.steps * NL)
     t_dn = ms_dn * 1e-3 / (args.steps * NL)
     gu_gbs = GU_BYTES / t_gu / 1e9
@@ -243,7 +250,7 @@ def main():
     torch.cuda.empty_cache()
 
     if not args.no_prefill:
-        out["mfma_peak"] = bench_mfma_peak(L, torch, q4mi)
+        out["mfma_peak"] = bench_mfma_peak(M, torch, q4mi)
         out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
         out["prefill"]["pct_of_measured_int8_peak"] = round(
             100 * out["prefill"]["mmq_TOPS"] / out["mfma_peak"]["int8_TOPS"], 2)
@@ -266,12 +273,12 @@ def bench_mfma_peak(L, torch, q4mi, iters=16384, reps=5):
     res = {}
     for kind, key in ((0, "int8_TOPS"), (1, "fp16_TFLOPS")):
         ops = ctypes.c_uint64(0)
-        q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe")
+        q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe", L)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
-            q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe")
+            q4mi.check(L.q4mi_mfma_probe(kind, iters, ctypes.byref(ops)), "mfma probe", L)
         e1.record()
         torch.cuda.synchronize()
         t = e0.elapsed_time(e1) * 1e-3 / reps

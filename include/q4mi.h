@@ -76,16 +76,19 @@ bool q4mi_mmvq(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
 
 /* Size library scratch before any graph capture (src/q4.h:958). */
 void q4_hip_moe_scratch_warm(void);
-/* Measurement hook: 1 = gate/up launch only, 2 = down only, 3 = both
- * (default).  No reference counterpart. */
-void q4mi_moe_phases(int mask);
-/* Test hook: cap the decode kernels' LDS at `bytes` (0: all of it), so their
- * LDS rings get reused within a launch.  No reference counterpart. */
-void q4mi_moe_lds_cap(uint32_t bytes);
-/* Measurement hook (no reference counterpart): one launch of an MFMA
- * throughput probe on the library stream (kind 0: int8 32x32x32, 1: fp16
- * 32x32x16); *ops = the launch's ops, for a caller-timed rate. */
-bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops);
+/* Drain the library stream and return the decode kernels' timeout word: 0
+ * when every bounded in-kernel wait completed; otherwise a wait gave up and
+ * the results of the decode calls since the last check are wrong (the bits
+ * are described by q4mi_status_text, which also becomes q4mi_last_error()).
+ * clear != 0 resets the word.  No reference counterpart (the reference's
+ * kernels have no bounded waits). */
+uint32_t q4mi_device_status(int clear);
+const char *q4mi_status_text(uint32_t bits);
+/* Copy the fp32 h = silu(gate.q8(x)) * (up.q8(x)) of the last decode call,
+ * [64 unique experts][8 tokens][n_ff], unique experts in first-appearance
+ * order, to d_dst (device) on the library stream.  Debug export (the
+ * reference keeps h in the caller's d_h, src/q4_rocm.cu:5444-5455). */
+bool q4mi_moe_copy_h(float *d_dst, uint32_t n_ff);
 /* One token; slots/wts are HOST arrays of n <= 64 experts.
  * d_y[r] += sum_e wts[e] * down_e(q8(silu(gate_e.q8(x)) * up_e.q8(x))).
  * gt == ut; IQ3_S or Q8_0; in_dim == n_embd.  d_h, d_h2, d_down are

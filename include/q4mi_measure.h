@@ -1,0 +1,34 @@
+/* q4mi_measure.h -- hooks of the measurement build of the library
+ * (suzuku-engine-q4_amd/lib/libq4mi_meas.so, compiled with -DQ4MI_MEASURE).
+ *
+ * The product library (libq4mi.so) does not export these: each changes
+ * process-global behaviour (a benchmark that runs only one kernel of the
+ * decode pair, a test that shrinks the kernels' LDS), which no production
+ * caller may reach.  None has a reference counterpart.
+ */
+#ifndef Q4MI_MEASURE_H
+#define Q4MI_MEASURE_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Which launches of the decode pair run: 1 = gate/up only, 2 = down only,
+ * 3 = both (default).  Lets a benchmark time each kernel alone. */
+void q4mi_moe_phases(int mask);
+/* Cap the decode kernels' LDS at `bytes` (0: all of it), so their LDS rings
+ * get reused within a launch. */
+void q4mi_moe_lds_cap(uint32_t bytes);
+/* One launch of an MFMA throughput probe on the library stream (kind 0:
+ * int8 32x32x32, 1: fp16 32x32x16); *ops = the launch's ops, for a
+ * caller-timed rate. */
+bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4MI_MEASURE_H */

@@ -52,6 +52,8 @@ class Oracle:
         L.or_dot8.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _i8p, _f32p]
         L.or_dot8_rows.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                    _f32p, ctypes.c_uint32, _f32p]
+        L.or_dot8q_rows.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
+                                    _i8p, _f32p, ctypes.c_uint32, _f32p]
         L.or_softmax_topk.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _f32p]
         L.or_pack.argtypes = [_i32p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                               ctypes.c_uint32, _i32p, _i32p, _f32p, _u32p, _i32p, _u32p, _i32p]
@@ -89,6 +91,18 @@ class Oracle:
         nt = x.shape[0]
         y = np.empty((nt, rows), np.float32)
         assert self.L.or_dot8_rows(ty, _p(w, _u8p), rows, n, _p(x, _f32p), nt, _p(y, _f32p))
+        return y
+
+    def dot8q_rows(self, ty, w, rows, n, q, d):
+        """Rows of w dotted with pre-quantized activations: q [nt, n] codes,
+        d [nt, n/32] scales -> y [nt, rows]."""
+        q = np.ascontiguousarray(np.atleast_2d(q), dtype=np.int8)
+        d = np.ascontiguousarray(np.atleast_2d(d), dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        nt = q.shape[0]
+        y = np.empty((nt, rows), np.float32)
+        assert self.L.or_dot8q_rows(ty, _p(w, _u8p), rows, n, _p(q, _i8p), _p(d, _f32p), nt,
+                                    _p(y, _f32p))
         return y
 
     def softmax_topk(self, logits, k):

@@ -239,6 +239,21 @@ int or_dot8_rows(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t n,
     return 1;
 }
 
+/* or_dot8 over rows with the activations given already quantized: q
+ * [nt][n] int8 codes and d [nt][n/32] scales (the down projection fed with
+ * another implementation's q8(h), so its exact-integer part is compared
+ * independently of how h rounded). */
+int or_dot8q_rows(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t n,
+                  const int8_t *q, const float *d, uint32_t nt, float *y) {
+    const uint64_t rb = or_row_bytes(type, n);
+    if (!rb) return 0;
+    for (uint32_t t = 0; t < nt; t++)
+        for (uint64_t r = 0; r < rows; r++)
+            y[(uint64_t)t * rows + r] =
+                or_dot8(type, w + r * rb, n, q + (uint64_t)t * n, d + (uint64_t)t * (n / 32));
+    return 1;
+}
+
 /* q4_softmax (serial sum, index order) then q4_topk with renormalisation:
  * strict '>' so that the earlier index wins ties. */
 void or_softmax_topk(const float *logits, uint32_t n, uint32_t k, int32_t *ids,

@@ -437,13 +437,22 @@ __device__ inline void lds_st(uint32_t *p, uint32_t v) {
     *(volatile uint32_t *)p = v;
 }
 // Every wait is bounded: a block that would wait longer than about 0.1 s
-// gives up and runs on (its results are then wrong, which the parity tests
-// report), so a protocol error can never hang the device.
+// gives up and runs on, so a protocol error can never hang the device.  Its
+// results are then wrong, and the block records that in g_moe_status (bit
+// kStConsumer / kStProducer), which q4mi_device_status() reads back after
+// the stream drained and reports through q4mi_last_error().
 constexpr uint32_t kSpinMax = 1u << 22;
+constexpr uint32_t kStConsumer = 1u;   // a consumer wait timed out
+constexpr uint32_t kStProducer = 2u;   // a producer's slot wait timed out
+__device__ uint32_t g_moe_status;
+
+__device__ inline void note_timeout(uint32_t bit) { atomicOr(&g_moe_status, bit); }
 
 // Wait until *p >= v; later LDS reads stay after the poll.
 __device__ inline void spin_ge(const uint32_t *p, uint32_t v) {
-    for (uint32_t n = 0; lds_ld(p) < v && n < kSpinMax; n++) __builtin_amdgcn_s_sleep(1);
+    uint32_t n = 0;
+    for (; lds_ld(p) < v && n < kSpinMax; n++) __builtin_amdgcn_s_sleep(1);
+    if (n == kSpinMax) note_timeout(kStConsumer);
     asm volatile("" ::: "memory");
 }
 __device__ inline void wait_chunk(const Sync *y, uint32_t c) {
@@ -485,6 +494,7 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
             idle++;
         }
     }
+    if (pub < C) note_timeout(kStProducer);
     wait_vm(0);
 }
 
@@ -1239,12 +1249,53 @@ static bool stage_ready() {
 
 extern "C" {
 
-/* Benchmark hook: 1 = gate/up launch only, 2 = down only, 3 = both. */
+#ifdef Q4MI_MEASURE
+/* Measurement build only (libq4mi_meas.so): 1 = gate/up launch only, 2 =
+ * down only, 3 = both. */
 void q4mi_moe_phases(int mask) { g_phases = mask & 3; }
 
-/* Test hook: cap the decode kernels' LDS at `bytes` (0: the CU's 160 KB), so
- * that their LDS rings are reused within a launch. */
+/* Measurement build only: cap the decode kernels' LDS at `bytes` (0: the
+ * CU's 160 KB), so that their LDS rings are reused within a launch. */
 void q4mi_moe_lds_cap(uint32_t bytes) { g_lds_cap = bytes; }
+#endif
+
+/* Copy the fp32 h of the last decode call, [64 unique experts][8 tokens]
+ * [n_ff] (unique experts in first-appearance order), to d_dst on the
+ * library stream.  A read-only debug export. */
+bool q4mi_moe_copy_h(float *d_dst, uint32_t n_ff) {
+    const size_t n = (size_t)kMaxU * kMaxT * n_ff;
+    if (!d_dst || !n_ff || scratch().pd_floats < n) {
+        set_error("q4mi_moe_copy_h: no decode h of that size");
+        return false;
+    }
+    if (hipMemcpyAsync(d_dst, scratch().pd, n * sizeof(float), hipMemcpyDeviceToDevice,
+                       stream()) != hipSuccess) {
+        set_error("q4mi_moe_copy_h: copy failed");
+        return false;
+    }
+    return true;
+}
+
+/* Drain the library stream and read the decode kernels' timeout word (0:
+ * every bounded wait completed; else the bits of q4mi_status_text).  A
+ * non-zero word also becomes q4mi_last_error(); clear != 0 resets it. */
+uint32_t q4mi_device_status(int clear) {
+    uint32_t v = 0;
+    if (hipStreamSynchronize(stream()) != hipSuccess ||
+        hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_moe_status), sizeof v, 0,
+                            hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error("q4mi_device_status: device not readable");
+        return 0x80000000u;
+    }
+    if (v) set_error("%s", q4mi_status_text(v));
+    if (v && clear) {
+        const uint32_t z = 0;
+        if (hipMemcpyToSymbol(HIP_SYMBOL(g_moe_status), &z, sizeof z, 0,
+                              hipMemcpyHostToDevice) != hipSuccess)
+            set_error("q4mi_device_status: reset failed");
+    }
+    return v;
+}
 
 /* Allocate the decode scratch (call before any stream capture). */
 void q4_hip_moe_scratch_warm(void) {

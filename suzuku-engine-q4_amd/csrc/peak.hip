@@ -11,6 +11,9 @@
 
 #include "q4mi_internal.h"
 
+// Built into the measurement library (libq4mi_meas.so, -DQ4MI_MEASURE) only.
+#ifdef Q4MI_MEASURE
+
 namespace q4mi {
 
 typedef int pk_v4i __attribute__((ext_vector_type(4)));
@@ -101,3 +104,5 @@ bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops) {
 }
 
 }  // extern "C"
+
+#endif  // Q4MI_MEASURE

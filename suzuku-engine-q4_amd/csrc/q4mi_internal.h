@@ -4,6 +4,11 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include "../../include/q4mi.h"
+#ifdef Q4MI_MEASURE
+#include "../../include/q4mi_measure.h"
+#endif
+
 namespace q4mi {
 
 // Stream every entry point launches on (q4_hip_stream / q4mi_set_stream).

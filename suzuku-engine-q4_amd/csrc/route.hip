@@ -38,10 +38,11 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
 }
 
 // One wave per token; up to 512 experts (8 per lane), k <= 64.
-// Ranking uses (logit desc, index asc): softmax is monotonic, so this is the
-// host's (probability desc, index asc) order except where two different
-// logits round to the same probability.  Weights: p_i = e_i * (1/sum e),
-// then p_i * (1/sum of the k picked p, in rank order).
+// Ranking uses the rounded probabilities p_i = e_i * (1/sum e) with the
+// lower index winning ties, as q4_topk does (src/q4_quant.c:728-750): two
+// different logits whose probabilities round to the same value (near-equal
+// logits, or probabilities that underflow to 0) go to the lower index.
+// Weights: p_i * (1/sum of the k picked p, in rank order).
 __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits, uint32_t n_tok,
                                                uint32_t n_exp, uint32_t topk,
                                                int32_t *__restrict__ ids,
@@ -74,12 +75,17 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
     for (int j = 0; j < 8; j++)
         if ((lane + 64u * j) < n_exp) alive |= 1u << j;
     const uint32_t tk = topk < n_exp ? topk : n_exp;
+    // p >= 0, so its key is its bit pattern with the top bit set (a live
+    // zero still outranks a dead entry's key 0)
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) pk[j] = __float_as_uint(e[j] * inv) | 0x80000000u;
     for (uint32_t k = 0; k < tk; k++) {
         // this lane's best alive entry: largest key, smallest index on ties
         uint32_t bk = 0, bj = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t key = (alive & (1u << j)) ? f2key(v[j]) : 0u;
+            const uint32_t key = (alive & (1u << j)) ? pk[j] : 0u;
             if (key > bk) {
                 bk = key;
                 bj = (uint32_t)j;

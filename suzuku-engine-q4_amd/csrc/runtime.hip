@@ -68,6 +68,17 @@ void q4mi_set_stream(void *s) { q4mi::g_stream = (hipStream_t)s; }
 
 const char *q4mi_last_error(void) { return q4mi::g_err; }
 
+const char *q4mi_status_text(uint32_t bits) {
+    static char buf[256];
+    if (!bits) return "ok";
+    if (bits & 0x80000000u) return "device status not readable";
+    snprintf(buf, sizeof buf, "decode kernel gave up a bounded wait (%s%s%s): results of the "
+             "calls since the last status check are wrong",
+             (bits & 1u) ? "consumer" : "", (bits & 3u) == 3u ? ", " : "",
+             (bits & 2u) ? "producer" : "");
+    return buf;
+}
+
 int q4mi_device_ok(void) {
     int n = 0;
     return hipGetDeviceCount(&n) == hipSuccess && n > 0;

@@ -17,6 +17,10 @@ import os
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # Q4MI_LIB selects another build of the same library (same ABI).
 LIB_PATH = os.environ.get("Q4MI_LIB") or os.path.join(PKG, "lib", "libq4mi.so")
+# The measurement build (-DQ4MI_MEASURE): the same ABI plus the hooks of
+# include/q4mi_measure.h.  Benchmarks and LDS-ring tests load it beside the
+# product library; its state (stream, scratch) is its own.
+MEAS_PATH = os.path.join(PKG, "lib", "libq4mi_meas.so")
 
 T_Q8_0 = 8
 T_IQ3_S = 21
@@ -44,9 +48,9 @@ _SIGS = {
     "q4_mmvq_n": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _f32, _u32]),
     "q4mi_mmvq": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _u32, _vp, _f32, _vp]),
     "q4_hip_moe_scratch_warm": (None, []),
-    "q4mi_moe_phases": (None, [_c.c_int]),
-    "q4mi_moe_lds_cap": (None, [_u32]),
-    "q4mi_mfma_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
+    "q4mi_device_status": (_u32, [_c.c_int]),
+    "q4mi_status_text": (_c.c_char_p, [_u32]),
+    "q4mi_moe_copy_h": (_b, [_vp, _u32]),
     "q4_hip_moe_exec": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32, _u64,
                              _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_exec_dev": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u64, _u32, _u64, _u32, _u64,
@@ -89,29 +93,52 @@ _SIGS = {
     "q4mi_expert_reduce_x": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u64, _vp]),
 }
 
+# measurement build only
+_MEAS_SIGS = {
+    "q4mi_moe_phases": (None, [_c.c_int]),
+    "q4mi_moe_lds_cap": (None, [_u32]),
+    "q4mi_mfma_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
+}
+
 _lib = None
+_meas = None
+
+
+def _load(path, sigs):
+    if not os.path.exists(path):
+        raise RuntimeError("q4mi: %s is missing; build it with __graft_entry__.build()" % path)
+    L = _c.CDLL(path)
+    for name, (res, args) in sigs.items():
+        f = getattr(L, name, None)
+        if f is None:
+            continue
+        f.restype = res
+        f.argtypes = args
+    return L
 
 
 def lib():
     """The loaded library (raises if it was not built: no silent fallback)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError("q4mi: %s is missing; build it with __graft_entry__.build()"
-                               % LIB_PATH)
-        L = _c.CDLL(LIB_PATH)
-        for name, (res, args) in _SIGS.items():
-            f = getattr(L, name, None)
-            if f is None:
-                continue
-            f.restype = res
-            f.argtypes = args
-        _lib = L
+        _lib = _load(LIB_PATH, _SIGS)
     return _lib
+
+
+def meas():
+    """The measurement build (product ABI + the measurement hooks)."""
+    global _meas
+    if _meas is None:
+        _meas = _load(MEAS_PATH, dict(_SIGS, **_MEAS_SIGS))
+    return _meas
 
 
 def exported_symbols():
     return list(_SIGS)
+
+
+def measurement_symbols():
+    return list(_MEAS_SIGS)
 
 
 def ptr(t):
@@ -123,20 +150,21 @@ def ptr(t):
     return t.data_ptr()
 
 
-def last_error():
-    e = lib().q4mi_last_error()
+def last_error(L=None):
+    e = (L or lib()).q4mi_last_error()
     return e.decode() if e else ""
 
 
-def check(ok, what):
+def check(ok, what, L=None):
     if not ok:
-        raise RuntimeError("%s failed: %s" % (what, last_error()))
+        raise RuntimeError("%s failed: %s" % (what, last_error(L)))
 
 
-def use_torch_stream():
-    """Launch on torch's current stream (so torch ops and ours are ordered)."""
+def use_torch_stream(L=None):
+    """Launch on torch's current stream (so torch ops and ours are ordered);
+    L: the library handle (default: the product library)."""
     import torch
-    lib().q4mi_set_stream(_c.c_void_p(torch.cuda.current_stream().cuda_stream))
+    (L or lib()).q4mi_set_stream(_c.c_void_p(torch.cuda.current_stream().cuda_stream))
 
 
 def row_bytes(ty, n):

@@ -1,7 +1,10 @@
 """Build the HIP library (gfx950) in-tree: lib/libq4mi.so.
 
 Every source under csrc/ is compiled by hipcc for gfx950 only and linked
-into one shared object exposing the C ABI declared in include/q4mi.h.
+into one shared object exposing the C ABI declared in include/q4mi.h.  The
+same sources compiled with -DQ4MI_MEASURE give lib/libq4mi_meas.so, which
+adds the measurement hooks of include/q4mi_measure.h (benchmarks and the
+LDS-ring tests load it; the product library never exports them).
 """
 import concurrent.futures as cf
 import glob
@@ -13,6 +16,7 @@ PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "lib", "libq4mi.so")
+MEAS_LIB = os.path.join(PKG, "lib", "libq4mi_meas.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -25,36 +29,49 @@ FLAGS = [
 ]
 
 
-def _compile(src):
-    obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+def _compile(job):
+    src, variant = job
+    obj = os.path.join(OBJ, variant, os.path.basename(src).replace(".hip", ".o"))
+    extra = ["-DQ4MI_MEASURE"] if variant == "meas" else []
+    cmd = [HIPCC] + FLAGS + extra + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l
                     and "target-feature" not in l)
     return obj, r.returncode, err
 
 
-def build(verbose=False):
-    os.makedirs(OBJ, exist_ok=True)
+def _link(objs, lib):
+    tmp = lib + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stderr)
+        raise RuntimeError("link failed: " + lib)
+    os.replace(tmp, lib)
+
+
+def build(verbose=False, measure=True):
+    variants = ["prod", "meas"] if measure else ["prod"]
+    for v in variants:
+        os.makedirs(os.path.join(OBJ, v), exist_ok=True)
     os.makedirs(os.path.dirname(LIB), exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
-    objs = []
+    # the longest compiles first, so the pool stays busy to the end
+    srcs.sort(key=lambda p: -os.path.getsize(p))
+    work = [(s, v) for s in srcs for v in variants]
+    jobs = min(len(work), int(os.environ.get("MAX_JOBS", "8")))
+    objs = {v: [] for v in variants}
     with cf.ThreadPoolExecutor(jobs) as ex:
-        for obj, rc, err in ex.map(_compile, srcs):
+        for (src, v), (obj, rc, err) in zip(work, ex.map(_compile, work)):
             if rc != 0:
                 sys.stderr.write(err + "\n")
                 raise RuntimeError("hipcc failed for " + obj)
             if verbose and err.strip():
                 sys.stderr.write(err + "\n")
-            objs.append(obj)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        sys.stderr.write(r.stderr)
-        raise RuntimeError("link failed")
-    os.replace(tmp, LIB)
+            objs[v].append(obj)
+    _link(objs["prod"], LIB)
+    if measure:
+        _link(objs["meas"], MEAS_LIB)
     return LIB
 
 

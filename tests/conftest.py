@@ -43,6 +43,17 @@ def gpu():
     return L
 
 
+@pytest.fixture(scope="session")
+def gpu_meas(gpu):
+    """The measurement build (product ABI + include/q4mi_measure.h hooks) on
+    the same stream."""
+    import q4mi
+    M = q4mi.meas()
+    assert M.q4mi_device_ok()
+    q4mi.use_torch_stream(M)
+    return M
+
+
 def layer_err(got, ref):
     """max |got-ref| / max|ref| (normwise)."""
     got = np.asarray(got, np.float64)

@@ -92,3 +92,39 @@ def test_boundary_extras_reject_without_gpu():
     assert not L.q4_mmq_gather(1, 0, 0, 100, 0, 100, 50, 100, 1, 1, 1, 1, 1)
     assert L.q4_mmq_gather(None, 0, 0, 0, 0, 0, 0, 0, None, None, 0, None, None)   # n = 0
     assert not L.q4_mmq_wbuf(1, 1, 0, None, None)
+
+
+MEAS_HEADER = os.path.join(ROOT, "include", "q4mi_measure.h")
+
+
+def _exports(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return set(l.split()[-1] for l in out.splitlines() if " T " in l)
+
+
+def test_measurement_hooks_only_in_measurement_build():
+    """The hooks that change process-global behaviour (run one kernel of the
+    decode pair, shrink the decode LDS, the MFMA probe) are exported by the
+    measurement build only; it also carries the whole product ABI."""
+    text = re.sub(r"/\*.*?\*/", "", open(MEAS_HEADER).read(), flags=re.S)
+    hooks = sorted(set(re.findall(r"\b(q4mi_\w+)\s*\(", text)))
+    assert hooks == sorted(q4mi.measurement_symbols())
+    prod = _exports(q4mi.LIB_PATH)
+    assert not [h for h in hooks if h in prod]
+    assert os.path.exists(q4mi.MEAS_PATH), "build the library first"
+    meas = _exports(q4mi.MEAS_PATH)
+    assert not [n for n in declared() + hooks if n not in meas]
+
+
+def test_status_text():
+    """The timeout word of the decode kernels' bounded waits, as text
+    (q4mi_device_status sets it as the last error when a wait gave up)."""
+    L = q4mi.lib()
+    assert L.q4mi_status_text(0) == b"ok"
+    t1 = L.q4mi_status_text(1).decode()
+    assert "consumer" in t1 and "producer" not in t1 and "wrong" in t1
+    t2 = L.q4mi_status_text(2).decode()
+    assert "producer" in t2 and "consumer" not in t2
+    assert "consumer, producer" in L.q4mi_status_text(3).decode()
+    assert "not readable" in L.q4mi_status_text(0x80000000).decode()

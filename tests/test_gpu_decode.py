@@ -255,7 +255,7 @@ def test_moe_decode_config2(gpu, oracle):
     assert np.array_equal(y.view(np.uint32), y3.view(np.uint32))
 
 
-def test_ring_reuse_matches(gpu, oracle):
+def test_ring_reuse_matches(gpu_meas, oracle):
     """Decode kernels whose LDS ring is smaller than their share (chunks reuse
     slots; 3 slots for 4 producers, where a slot's successive chunks belong
     to different producers) give the unconstrained run's y bit for bit:
@@ -281,11 +281,11 @@ def test_ring_reuse_matches(gpu, oracle):
     d_wid, d_wwt, d_wn, dxw = dev(wes), dev(wew), dev(np.full(4, 10, np.int32)), dev(xw)
 
     def run(window=True, devlist=True):
-        y_host = moe_exec_host(gpu, ly, x, ids, wts)
+        y_host = moe_exec_host(gpu_meas, ly, x, ids, wts)
         if not devlist:
             return [y_host]
         yd = dev(np.zeros(ly.n_embd, np.float32))
-        q4mi.check(gpu.q4_hip_moe_exec_dev(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es),
+        q4mi.check(gpu_meas.q4_hip_moe_exec_dev(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_es),
                                            q4mi.ptr(d_ew), q4mi.ptr(d_n), T_IQ3_S, ly.og,
                                            T_IQ3_S, ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dx), None,
                                            None, None, q4mi.ptr(yd), ly.n_ff, ly.n_embd,
@@ -293,7 +293,7 @@ def test_ring_reuse_matches(gpu, oracle):
         if not window:
             return [y_host, host(yd)]
         yw = dev(np.zeros((4, ly.n_embd), np.float32))
-        q4mi.check(gpu.q4_hip_moe_exec_win(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_wid),
+        q4mi.check(gpu_meas.q4_hip_moe_exec_win(q4mi.ptr(ly.d_arena), ly.stride, q4mi.ptr(d_wid),
                                            q4mi.ptr(d_wwt), q4mi.ptr(d_wn), 4, T_IQ3_S, ly.og,
                                            T_IQ3_S, ly.ou, T_IQ3_S, ly.od, q4mi.ptr(dxw), None,
                                            q4mi.ptr(yw), ly.n_ff, ly.n_embd, ly.n_embd),
@@ -306,11 +306,11 @@ def test_ring_reuse_matches(gpu, oracle):
         # 80 KB: the device list's down ring does (3 slots, 8 chunks);
         # 70 / 59 KB: the host list's gate/up ring does (3 or 4 slots)
         for cap in (120000, 81920, 72000, 60000):
-            gpu.q4mi_moe_lds_cap(cap)
+            gpu_meas.q4mi_moe_lds_cap(cap)
             for got, want in zip(run(window=cap >= 120000, devlist=cap >= 81920), base):
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), cap
     finally:
-        gpu.q4mi_moe_lds_cap(0)
+        gpu_meas.q4mi_moe_lds_cap(0)
 
 
 def test_moe_exec_dev_and_rejects(gpu, oracle):

@@ -49,6 +49,39 @@ def test_route_matches_oracle(gpu, oracle, T, E, k, zipf):
     assert np.allclose(wts, ow, rtol=1e-6, atol=1e-9)
 
 
+def test_route_probability_ties(gpu, oracle, ref):
+    """Different logits whose probabilities round to the same value go to the
+    lower index, as q4_topk ranks them (src/q4_quant.c:728-750):
+    - logits 1 ulp apart right at the maximum (both exp to exactly 1.0);
+    - a token where only 4 experts have a non-zero probability: the other
+      6 picks are the lowest-index experts among the underflowed ones,
+      whatever their logits."""
+    E, k = 512, 10
+    rng = np.random.default_rng(5)
+    lg = np.stack([rng.standard_normal(E) for _ in range(3)]).astype(np.float32)
+    # token 0: the maximum 1e-3 at index 300, its 1-ulp-lower neighbour at 7
+    # and 200 (lower index), and at 450; exp(-1 ulp) rounds to 1.0
+    lg[0] = rng.uniform(-30, -20, E).astype(np.float32)
+    top = np.float32(1e-3)
+    lg[0, 300] = top
+    lg[0, [7, 450]] = np.nextafter(top, np.float32(-1))
+    lg[0, 200] = np.nextafter(np.nextafter(top, np.float32(-1)), np.float32(-1))
+    # token 1: 4 live experts; the rest sit 200..300 below (exp underflows
+    # to 0), with the larger of those logits at the higher indices
+    lg[1] = (-200.0 - np.linspace(100, 0, E)).astype(np.float32)
+    lg[1, [11, 99, 300, 480]] = [1.0, 0.5, 0.25, 2.0]
+    # token 2: all equal
+    lg[2] = 0.75
+    ids, wts = route_gpu(gpu, lg, k)
+    oid, ow = oracle.softmax_topk(lg, k)
+    rid, rw = ref.softmax_topk(lg, k)
+    assert np.array_equal(oid, rid) and np.array_equal(ow.view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(ids, oid)
+    assert list(oid[1, 4:]) == [0, 1, 2, 3, 4, 5]
+    assert list(oid[2]) == list(range(10))
+    assert np.allclose(wts, ow, rtol=1e-6, atol=1e-9)
+
+
 def test_softmax_topk_host_copy(gpu, oracle):
     rng = np.random.default_rng(3)
     lg = rng.standard_normal(512).astype(np.float32)

@@ -222,3 +222,18 @@ def test_moe_window_vs_reference(oracle, ref):
                      np.full(T, k, np.uint32))
     yo = oracle.moe_tokens(n_embd, n_ff, T_IQ3_S, T_IQ3_S, arena, stride, x, ids, wts)
     assert rel_err(yo, yr) < 1e-5
+
+
+def test_dot8q_rows_is_dot8_of_quantized(oracle):
+    """or_dot8q_rows (pre-quantized activations) equals or_dot8_rows bit for
+    bit when fed or_quant8's codes and scales."""
+    from q4mi import synth
+    rng = np.random.default_rng(8)
+    for ty, K in ((om.T_IQ3_S, 512), (om.T_Q8_0, 256)):
+        w = synth.matrix(rng, ty, 40, K)
+        x = rng.standard_normal((3, K)).astype(np.float32)
+        q = np.stack([oracle.quant8(x[t])[0] for t in range(3)])
+        d = np.stack([oracle.quant8(x[t])[1] for t in range(3)])
+        a = oracle.dot8q_rows(ty, w, 40, K, q, d)
+        b = oracle.dot8_rows(ty, w, 40, K, x)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
