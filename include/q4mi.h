@@ -99,6 +99,17 @@ bool q4_hip_moe_exec(const uint8_t *base, uint64_t stride, const int32_t *slots,
                      uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_h,
                      float *d_h2, float *d_down, float *d_y, uint32_t n_ff, uint32_t in_dim,
                      uint32_t n_embd);
+/* q4_hip_moe_exec that allocates nothing, for callers that cannot allocate
+ * (code under graph capture, serving loops that forbid hipMalloc): its
+ * intermediates (fp32 h and the list plan) live in a file-scope device
+ * array of 2 MiB + 4 KB per GPU, held until the process ends, so n_ff <=
+ * 1024 (larger is rejected before any launch).  No counterpart in the
+ * reference.  Calls that overlap on one GPU share that array and race; d_y
+ * is accumulated as by q4_hip_moe_exec (same kernels, same bits). */
+bool q4mi_moe_exec_noalloc(const uint8_t *base, uint64_t stride, const int32_t *slots,
+                           const float *wts, uint32_t n, uint32_t gt, uint64_t og, uint32_t ut,
+                           uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_y,
+                           uint32_t n_ff, uint32_t in_dim, uint32_t n_embd);
 /* Same with device lists (count d_nhit[0]); graph-capturable.  Replaces
  * q4_hip_moe_exec_dev (src/q4.h:1295-1301, src/q4_rocm.cu:6570-6608). */
 bool q4_hip_moe_exec_dev(const uint8_t *base, uint64_t stride, const int32_t *d_es,

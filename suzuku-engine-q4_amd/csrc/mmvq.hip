@@ -201,7 +201,7 @@ bool q4_mmvq_n(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
         return mmvq_f32(ty, d_w, nrows, ncols, d_x, n, d_y, scale);
     }
     if (!ensure_xq((size_t)8 * 8192)) return false;
-    Scratch &s = scratch();
+    Scratch &s = lib_scratch();
     const bool reuse = g_hold && g_hold == d_x && g_cur_x == d_x && g_cur_k == ncols &&
                        g_cur_n >= n;
     if (!reuse) {

@@ -1153,12 +1153,19 @@ bool moe_warm(uint32_t n_ff) {
     return ensure_pd((size_t)kMaxU * kMaxT * n_ff);
 }
 
+// Where a call's intermediates live: the fp32 h [kMaxU][kMaxT][n_ff] and the
+// device-list plan.  Null: the library's lazily allocated scratch.
+struct Work {
+    float *h;
+    Plan *plan;
+};
+
 // Common driver.  All checks happen before the first launch so that a false
 // return never leaves half of the work queued.
 static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
                     const HostList &hl, uint32_t nu_host, uint32_t gt, uint64_t og, uint32_t ut,
                     uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_y,
-                    uint32_t n_ff, uint32_t in_dim, uint32_t n_embd) {
+                    uint32_t n_ff, uint32_t in_dim, uint32_t n_embd, Work work = Work{}) {
     if (!base || !d_x || !d_y || src.n_tok < 1 || src.n_tok > kMaxT) {
         set_error("moe: bad arguments");
         return false;
@@ -1180,7 +1187,7 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
         set_error("moe: expert arena offsets must be 4-byte aligned");
         return false;
     }
-    if (!moe_warm(n_ff)) return false;
+    if (!work.h && !moe_warm(n_ff)) return false;
     MoeArgs a = {};
     a.base = base;
     a.stride = stride;
@@ -1193,14 +1200,14 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     a.rb_gu = (uint32_t)q4mi_row_bytes(gt, in_dim);
     a.rb_dn = (uint32_t)q4mi_row_bytes(dt, n_ff);
     a.x = d_x;
-    a.h = scratch().pd;
+    a.h = work.h ? work.h : lib_scratch().pd;
     a.y = d_y;
     a.src = src;
     a.hl = hl;
-    a.gplan = g_plan;
+    a.gplan = work.h ? work.plan : g_plan;
     a.plan_in = (g_phases & 1) ? 1u : 0u;   // down follows this call's gate/up
 #ifdef Q4MI_TRACE
-    if (!g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
+    if (!work.h && !g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
         (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
     a.trace = g_trace;
 #endif
@@ -1227,6 +1234,68 @@ struct StageList {
     int32_t n;
 };
 static StageList *g_stage = nullptr, *g_stage_dev = nullptr;
+
+// Unique ids of a host list in first-appearance order; a repeated id adds its
+// weights (the reference computes every entry and sums them).  Returns the
+// unique count.
+static uint32_t host_list(const int32_t *slots, const float *wts, uint32_t n, HostList &hl) {
+    uint32_t nu = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (slots[i] < 0) continue;
+        uint32_t u = 0;
+        while (u < nu && hl.id[u] != slots[i]) u++;
+        if (u == nu) {
+            hl.id[nu++] = slots[i];
+            hl.w[u] = wts[i];
+        } else {
+            hl.w[u] += wts[i];
+        }
+    }
+    for (uint32_t i = nu; i < kMaxU; i++) {
+        hl.id[i] = -1;
+        hl.w[i] = 0.f;
+    }
+    return nu;
+}
+
+// ------------------------------------------------ allocation-free decode
+// q4mi_moe_exec_noalloc keeps its intermediates in this file-scope device
+// array instead of library allocations: the device-list plan (unused by a
+// host list, but the kernels take its address) then the fp32 h of up to 64
+// unique experts x 8 token rows x n_ff <= 1024.  Each GPU holds its own copy
+// for the life of the process; in host code `scratch` is only a stand-in
+// symbol, so its device address is looked up once per device
+// (hipGetSymbolAddress) and only that address reaches the kernels.  Nothing
+// in it needs to start at zero: every call's gate/up launch writes every h
+// row its down launch reads.
+constexpr size_t kNaPlanBytes = (sizeof(Plan) + 255) & ~(size_t)255;
+constexpr uint32_t kNaMaxFF = 1024;
+constexpr size_t kNaBytes = kNaPlanBytes + (size_t)kMaxU * kMaxT * kNaMaxFF * sizeof(float);
+
+static __device__ __align__(256) uint8_t scratch[kNaBytes];
+
+constexpr int kNaMaxDev = 64;
+static uint8_t *g_na_ptr[kNaMaxDev];
+
+// The current device's address of `scratch` (looked up on its first use).
+static uint8_t *noalloc_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNaMaxDev) {
+        set_error("q4mi_moe_exec_noalloc: no usable current device");
+        return nullptr;
+    }
+    if (!g_na_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("q4mi_moe_exec_noalloc: hipGetSymbolAddress failed: %s",
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_na_ptr[dev] = (uint8_t *)p;
+    }
+    return g_na_ptr[dev];
+}
 
 static bool stage_ready() {
     if (g_stage) return true;
@@ -1264,11 +1333,11 @@ void q4mi_moe_lds_cap(uint32_t bytes) { g_lds_cap = bytes; }
  * library stream.  A read-only debug export. */
 bool q4mi_moe_copy_h(float *d_dst, uint32_t n_ff) {
     const size_t n = (size_t)kMaxU * kMaxT * n_ff;
-    if (!d_dst || !n_ff || scratch().pd_floats < n) {
+    if (!d_dst || !n_ff || lib_scratch().pd_floats < n) {
         set_error("q4mi_moe_copy_h: no decode h of that size");
         return false;
     }
-    if (hipMemcpyAsync(d_dst, scratch().pd, n * sizeof(float), hipMemcpyDeviceToDevice,
+    if (hipMemcpyAsync(d_dst, lib_scratch().pd, n * sizeof(float), hipMemcpyDeviceToDevice,
                        stream()) != hipSuccess) {
         set_error("q4mi_moe_copy_h: copy failed");
         return false;
@@ -1319,29 +1388,41 @@ bool q4_hip_moe_exec(const uint8_t *base, uint64_t stride, const int32_t *slots,
         set_error("q4_hip_moe_exec: bad expert list");
         return false;
     }
-    // unique ids in first-appearance order; a repeated id adds its weights
-    // (the reference computes every entry and sums them)
     HostList hl;
-    uint32_t nu = 0;
-    for (uint32_t i = 0; i < n; i++) {
-        if (slots[i] < 0) continue;
-        uint32_t u = 0;
-        while (u < nu && hl.id[u] != slots[i]) u++;
-        if (u == nu) {
-            hl.id[nu++] = slots[i];
-            hl.w[u] = wts[i];
-        } else {
-            hl.w[u] += wts[i];
-        }
-    }
-    for (uint32_t i = nu; i < kMaxU; i++) {
-        hl.id[i] = -1;
-        hl.w[i] = 0.f;
-    }
+    const uint32_t nu = host_list(slots, wts, n, hl);
     if (!nu) return true;
     ListSrc src = {nullptr, nullptr, nullptr, kMaxU, 1, nu, 1};
     return moe_run(base, stride, src, hl, nu, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
                    n_embd);
+}
+
+/* q4_hip_moe_exec that allocates nothing: its intermediates live in the
+ * file-scope device array `scratch` (2 MiB + the plan, n_ff <= 1024), so a
+ * caller that cannot allocate (under graph capture, in a serving loop that
+ * forbids hipMalloc) can call it from the first call on.  Calls that overlap
+ * on one GPU share that array and race. */
+bool q4mi_moe_exec_noalloc(const uint8_t *base, uint64_t stride, const int32_t *slots,
+                           const float *wts, uint32_t n, uint32_t gt, uint64_t og, uint32_t ut,
+                           uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_y,
+                           uint32_t n_ff, uint32_t in_dim, uint32_t n_embd) {
+    if (!slots || !wts || !n || n > kMaxU) {
+        set_error("q4mi_moe_exec_noalloc: bad expert list");
+        return false;
+    }
+    if (n_ff > kNaMaxFF) {
+        set_error("q4mi_moe_exec_noalloc: n_ff %u needs %zu bytes of h, beyond the %zu-byte "
+                  "static scratch (n_ff <= %u)", n_ff, (size_t)kMaxU * kMaxT * n_ff * 4,
+                  kNaBytes - kNaPlanBytes, kNaMaxFF);
+        return false;
+    }
+    HostList hl;
+    const uint32_t nu = host_list(slots, wts, n, hl);
+    if (!nu) return true;
+    uint8_t *sp = noalloc_scratch();
+    if (!sp) return false;
+    ListSrc src = {nullptr, nullptr, nullptr, kMaxU, 1, nu, 1};
+    return moe_run(base, stride, src, hl, nu, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
+                   n_embd, Work{(float *)(sp + kNaPlanBytes), (Plan *)sp});
 }
 
 /* Same, with slots/weights/count in device memory (count d_nhit[0]). */

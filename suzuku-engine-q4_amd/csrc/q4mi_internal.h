@@ -26,7 +26,7 @@ struct Scratch {
     float *xd = nullptr;
     size_t xq_elems = 0;
 };
-Scratch &scratch();
+Scratch &lib_scratch();
 bool ensure_pd(size_t floats);
 bool ensure_tickets(size_t n);
 bool ensure_xq(size_t elems);

@@ -11,7 +11,7 @@ static Scratch g_scr;
 static char g_err[512];
 
 hipStream_t stream() { return g_stream; }
-Scratch &scratch() { return g_scr; }
+Scratch &lib_scratch() { return g_scr; }
 
 void set_error(const char *fmt, ...) {
     va_list ap;

@@ -53,6 +53,8 @@ _SIGS = {
     "q4mi_moe_copy_h": (_b, [_vp, _u32]),
     "q4_hip_moe_exec": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32, _u64,
                              _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4mi_moe_exec_noalloc": (_b, [_vp, _u64, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
+                                   _u64, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_exec_dev": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u64, _u32, _u64, _u32, _u64,
                                  _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_win_ok": (_b, [_u32, _u32, _u32, _u32, _u32, _u32]),
