@@ -164,6 +164,27 @@ bool q4_hip_softmax_topk_launch(const float *d_logits, uint32_t n, uint32_t k, i
                                 float *d_wts);
 bool q4_hip_softmax_topk(const float *d_logits, uint32_t n, uint32_t k, int32_t *h_ids,
                          float *h_wts);
+/* Router front of a MoE layer, one entry for decode, verify windows and
+ * prefill: logits[t][e] = W_r[e] . x[t] (the router GEMV; W_r is n_exp rows
+ * of n_embd in F32 (type 0), F16 (1) or BF16 (30), dot order fixed so the
+ * logits reproduce bit for bit), then softmax + top-k + renormalisation as
+ * q4_hip_route_pf into ids/wts rows of ostride entries.  With d_sgw (the
+ * shared expert's gate vector, fp32 [n_embd]) also d_sg[t] =
+ * sigmoid(d_sgw . x[t]).  With shared_slot >= 0 each token's row gets one
+ * more entry after its topk picks: expert shared_slot with weight d_sg[t]
+ * (1 without a gate), so the shared expert runs inside the same decode /
+ * window launch; d_nh (optional) receives the per-token entry counts.  With
+ * ostride 64 the rows are the device lists of q4_hip_moe_exec_win /
+ * q4_hip_moe_exec_dev.  n_exp <= 512, topk <= 64, n_embd % 256 == 0 and <=
+ * 16384, pointers 16-byte aligned.  Replaces the router q4_hip_gemv_dd +
+ * q4_hip_moe_pack sgate dot + route_dev_n_k sequence of q4_moe_gpu_a /
+ * q4_moe_gpu_dev (src/q4_moe.c:1360-1440, src/q4_rocm.cu:5930-6060,
+ * :15967-15990); the gate is applied as y += sg * shared
+ * (src/q4_moe.c:297-306). */
+bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, const float *d_x,
+                    uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                    float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
+                    uint32_t ostride, int32_t shared_slot, float *d_sg);
 /* Stable expert pack per token group: the host order of src/q4_moe.c:
  * 3404-3451 (the reference's GPU assign_pf_k orders by atomic arrival).
  * Replaces q4_hip_assign_pf (src/q4.h:1281-1285, src/q4_rocm.cu:6483-6563). */

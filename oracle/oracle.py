@@ -54,6 +54,8 @@ class Oracle:
                                    _f32p, ctypes.c_uint32, _f32p]
         L.or_dot8q_rows.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                     _i8p, _f32p, ctypes.c_uint32, _f32p]
+        L.or_router.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_uint32, _f32p,
+                                ctypes.c_uint32, _f32p, _f32p, _f32p]
         L.or_softmax_topk.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _f32p]
         L.or_pack.argtypes = [_i32p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                               ctypes.c_uint32, _i32p, _i32p, _f32p, _u32p, _i32p, _u32p, _i32p]
@@ -104,6 +106,20 @@ class Oracle:
         assert self.L.or_dot8q_rows(ty, _p(w, _u8p), rows, n, _p(q, _i8p), _p(d, _f32p), nt,
                                     _p(y, _f32p))
         return y
+
+    def router(self, ty, w, n_exp, K, x, sgw=None):
+        """Router logits [T, n_exp] (and the shared-expert gate sg [T] when
+        sgw is given) in the library's fixed dot order."""
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+        T = x.shape[0]
+        lg = np.empty((T, n_exp), np.float32)
+        sg = np.empty(T, np.float32)
+        g = None if sgw is None else np.ascontiguousarray(sgw, dtype=np.float32)
+        assert self.L.or_router(ty, _p(w, _u8p), n_exp, K, _p(x, _f32p), T,
+                                None if g is None else _p(g, _f32p), _p(lg, _f32p),
+                                _p(sg, _f32p))
+        return (lg, sg) if sgw is not None else lg
 
     def softmax_topk(self, logits, k):
         logits = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
@@ -167,6 +183,9 @@ class Ref:
                                                            ctypes.c_uint32, _i32p, _f32p,
                                                            _u32p, _f32p]
         L.qref_softmax_topk.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _f32p]
+        L.q4_gemv.restype = ctypes.c_bool
+        L.q4_gemv.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
+                              _f32p, ctypes.c_float]
 
     def quant8(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -206,6 +225,15 @@ class Ref:
         assert self.L.qref_moe_win(n_embd, n_ff, t_gu, t_d, n_exp, _p(arena, _u8p), stride,
                                    _p(x, _f32p), n_tok, _p(ids, _i32p), _p(wts, _f32p),
                                    _p(tn, _u32p), _p(y, _f32p))
+        return y
+
+    def gemv(self, ty, w, rows, cols, x):
+        """The reference's float GEMV q4_gemv (src/q4_quant.c:595-622): the
+        router logits of its CPU path."""
+        w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(rows, np.float32)
+        assert self.L.q4_gemv(ty, _p(w, _u8p), rows, cols, _p(x, _f32p), _p(y, _f32p), 1.0)
         return y
 
     def softmax_topk(self, logits, k):

@@ -254,6 +254,62 @@ int or_dot8q_rows(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t n,
     return 1;
 }
 
+/* Router GEMV (router.hip, q4mi_moe_route): logits[t][e] = W[e] . x[t] for a
+ * row type F32 (0), F16 (1) or BF16 (30), in the library's fixed order:
+ * lane l (of 64) sums, for i = 0 .. K/256-1, the four products at element
+ * 4(64i + l) with fmaf in component order; the 64 lane sums are joined by an
+ * xor butterfly over distances 32 .. 1.  The reference's router is the same
+ * GEMV (q4_gemv / dot_f32, src/q4_quant.c:583-622, in another order).  With
+ * sgw, sg[t] = 1 / (1 + expf(-(sgw . x[t]))) (src/q4_moe.c:297-306), same
+ * dot order. */
+static float or_rw(uint32_t type, const uint8_t *row, uint64_t i) {
+    if (type == 0) {
+        float f;
+        memcpy(&f, row + 4 * i, 4);
+        return f;
+    }
+    const uint16_t h = (uint16_t)(row[2 * i] | (row[2 * i + 1] << 8));
+    if (type == 1) return or_f16_to_f32(h);
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static float or_lane_dot(uint32_t type, const uint8_t *row, const float *x, uint32_t K) {
+    float acc[64], nx[64];
+    for (uint32_t l = 0; l < 64; l++) {
+        float a = 0.f;
+        for (uint32_t i = 0; i < K / 256; i++)
+            for (uint32_t c = 0; c < 4; c++) {
+                const uint64_t e = 4ull * (64 * i + l) + c;
+                a = fmaf(or_rw(type, row, e), x[e], a);
+            }
+        acc[l] = a;
+    }
+    for (uint32_t o = 32; o >= 1; o >>= 1) {
+        for (uint32_t l = 0; l < 64; l++) nx[l] = acc[l] + acc[l ^ o];
+        memcpy(acc, nx, sizeof acc);
+    }
+    return acc[0];
+}
+
+int or_router(uint32_t type, const uint8_t *w, uint32_t n_exp, uint32_t K, const float *x,
+              uint32_t T, const float *sgw, float *logits, float *sg) {
+    if ((type != 0 && type != 1 && type != 30) || K % 256) return 0;
+    const uint64_t rb = (uint64_t)K * (type == 0 ? 4 : 2);
+    for (uint32_t t = 0; t < T; t++) {
+        const float *xt = x + (uint64_t)t * K;
+        for (uint32_t e = 0; e < n_exp; e++)
+            logits[(uint64_t)t * n_exp + e] = or_lane_dot(type, w + e * rb, xt, K);
+        if (sgw) {
+            const float d = or_lane_dot(0, (const uint8_t *)sgw, xt, K);
+            sg[t] = 1.f / (1.f + expf(-d));
+        }
+    }
+    return 1;
+}
+
 /* q4_softmax (serial sum, index order) then q4_topk with renormalisation:
  * strict '>' so that the earlier index wins ties. */
 void or_softmax_topk(const float *logits, uint32_t n, uint32_t k, int32_t *ids,

@@ -344,6 +344,7 @@ struct MoeArgs {
     ListSrc src;
 #ifdef Q4MI_TRACE
     unsigned long long *trace;   // [2 kernels][4096 blocks][32] phase timestamps
+    uint32_t dbg;                // trace build experiments (Q4MI_DBG)
 #endif
     Plan *gplan;      // device list: the plan gate/up block 0 publishes for down
     uint32_t plan_in; // down: load gplan instead of building the plan
@@ -466,7 +467,14 @@ __device__ inline void wait_chunk(const Sync *y, uint32_t c) {
 // unpublished, so it cannot hold back a chunk the consumers are waiting for.
 template <class IssueFn, class ItemsFn>
 __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, uint32_t S,
-                               uint32_t &issued, IssueFn issue, ItemsFn items) {
+                               uint32_t &issued, IssueFn issue, ItemsFn items
+#ifdef Q4MI_TRACE
+                               , unsigned long long *q4tr = nullptr, uint32_t q4kern = 0
+#endif
+                               ) {
+#ifdef Q4MI_TRACE
+    const uint32_t q4bid = blockIdx.x;
+#endif
     uint32_t next = p, pub = p;    // next chunk to issue / to publish
     // Slot c % S is free for chunk c once chunk c - S (its previous user,
     // possibly another producer's) was issued there and fully consumed.  The
@@ -477,17 +485,30 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
                          lds_ld(&y->cons[c % S]) >= items(c - S));
     };
     uint32_t idle = 0;
+#ifdef Q4MI_TRACE
+    uint32_t npub = 0, nloop = 0;
+#endif
     while (pub < C && idle < kSpinMax) {
         while (next < C && (next < pub + kProd * kMaxS) && slot_free(next)) {
             if (next >= S) lds_st(&y->cons[next % S], 0);
             lds_st(&y->owner[next % S], next);
             issue(next);
+#ifdef Q4MI_TRACE
+            if (next / kProd < 3) Q4MI_TR(24 + next / kProd, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
+#endif
             ends[(next / kProd) % kMaxS] = issued;
             next += kProd;
         }
+#ifdef Q4MI_TRACE
+        if (nloop++ == 0) Q4MI_TR(20, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
+#endif
         if (pub < next) {
             wait_vm(issued - ends[(pub / kProd) % kMaxS]);
             lds_st(&y->landed[p], pub / kProd + 1);
+#ifdef Q4MI_TRACE
+            if (npub < 4) Q4MI_TR(21 + npub, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
+            npub++;
+#endif
             pub += kProd;
         } else {
             __builtin_amdgcn_s_sleep(1);   // every own chunk published; wait for a slot
@@ -538,7 +559,11 @@ __device__ inline void gu_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
         }
     };
     auto items = [&](uint32_t c) { return min(ch, np - c * ch); };
-    produce(Y, P->ends[wave], wave, C, S, issued, issue, items);
+    produce(Y, P->ends[wave], wave, C, S, issued, issue, items
+#ifdef Q4MI_TRACE
+            , a.trace, 0
+#endif
+    );
 }
 
 // Consumer prologue: q8 of x (v0 = quad ct, loaded by the caller), then
@@ -581,10 +606,25 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     XRegs<NT, GPT> xr;
     load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi);
     float *hout = a.h;
+#ifdef Q4MI_TRACE
+    unsigned long long *const q4tr = a.trace;
+    const uint32_t q4bid = blockIdx.x;
+    uint32_t round = 0;
+#endif
     for (uint32_t b = cw * kTpw; b < np; b += kTeams) {   // b: this wave's first pair
         const uint32_t bl = min(b + kTpw, np) - 1;
         for (uint32_t c = b / ch; c <= bl / ch; c++) wait_chunk(Y, c);
+#ifdef Q4MI_TRACE
+        if (round < 8) Q4MI_TR(5 + round, 0, ct == 0);
+        round++;
+#endif
         const uint32_t i = b + sub;
+#ifdef Q4MI_TRACE
+        if ((a.dbg & 1u) && i < np) {   // stream only: count the pair consumed
+            if (gi == TPR - 1) atomicAdd(&Y->cons[(i / ch) % S], 1u);
+            continue;
+        }
+#endif
         if (i < np) {
             const uint32_t c = i / ch, j = i % ch;
             const uint8_t *tile = ring + (size_t)(c % S) * slot_bytes;
@@ -703,6 +743,9 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     gu_compute<TY, NT, TPR, GPT>(a, stab, P, Y, xq, xd, ring, ch, S, p0, p1 - p0, uniq, ct,
                                  wave - kProd);
     Q4MI_TR(30, 0, ct == 0);
+#ifdef Q4MI_TRACE
+    if (lane == 0 && atomicAdd(&Y->ready, 1u) == 2 * kConsW - 1) Q4MI_TR(29, 0, true);
+#endif
 }
 
 // ---------------------------------------------------------------- down
@@ -734,7 +777,11 @@ __device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
         }
     };
     auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
-    produce(Y, P->ends[wave], wave, C, S, issued, issue, items);
+    produce(Y, P->ends[wave], wave, C, S, issued, issue, items
+#ifdef Q4MI_TRACE
+            , a.trace, 1
+#endif
+    );
 }
 
 // Consumers: q8 of every selected h row, the (expert, row) dots as their
@@ -782,6 +829,11 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
     }
     if (lane == 0) atomicAdd(&Y->ready, 1u);
     spin_ge(&Y->ready, kConsW);                     // table and q8(h) complete
+#ifdef Q4MI_TRACE
+    unsigned long long *const q4tr = a.trace;
+    const uint32_t q4bid = blockIdx.x;
+    Q4MI_TR(5, 1, ct == 0);
+#endif
     constexpr uint32_t kTeams = kCons / TPR, kTpw = 64 / TPR;
     const uint32_t gi = ct % TPR, sub = (ct & 63u) / TPR;
     const uint32_t ni = nu * nr;                    // items, expert-major
@@ -853,8 +905,14 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);
         }
     }
+#ifdef Q4MI_TRACE
+    Q4MI_TR(6, 1, ct == 0);
+#endif
     if (lane == 0) atomicAdd(&Y->fin, 1u);
     spin_ge(&Y->fin, kConsW);                       // every partial sum written
+#ifdef Q4MI_TRACE
+    Q4MI_TR(7, 1, ct == 0);
+#endif
     // y[t][r] += sum_u w[u][t] * part[u][t][r]: lane sl of an output's
     // 8 lanes takes experts u = sl, sl + 8, ... in plan order, then a fixed
     // DPP tree joins the 8 partial sums (deterministic)
@@ -1143,6 +1201,9 @@ static bool shape_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uin
 }
 
 static Plan *g_plan = nullptr;   // a device-list call's plan, gate/up -> down
+#ifdef Q4MI_TRACE
+static unsigned long long *g_trace = nullptr;
+#endif
 
 bool moe_warm(uint32_t n_ff) {
     if (!g_plan && hipMalloc(&g_plan, sizeof(Plan)) != hipSuccess) {
@@ -1210,6 +1271,7 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     if (!work.h && !g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
         (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
     a.trace = g_trace;
+    a.dbg = getenv("Q4MI_DBG") ? (uint32_t)atoi(getenv("Q4MI_DBG")) : 0u;
 #endif
     const uint32_t nt = src.n_tok;
     if (nt == 1) return run_nt<1>(gt, dt, a, nu_host);
@@ -1326,6 +1388,18 @@ void q4mi_moe_phases(int mask) { g_phases = mask & 3; }
 /* Measurement build only: cap the decode kernels' LDS at `bytes` (0: the
  * CU's 160 KB), so that their LDS rings are reused within a launch. */
 void q4mi_moe_lds_cap(uint32_t bytes) { g_lds_cap = bytes; }
+#endif
+
+#ifdef Q4MI_TRACE
+/* Trace build only: copy the phase timestamps [2 kernels][4096 blocks][32]
+ * (wall clock, 100 MHz) of the last traced call to host memory, and clear
+ * them. */
+bool q4mi_trace_read(unsigned long long *dst, uint64_t n) {
+    if (!g_trace || n > 2ull * 4096 * 32) return false;
+    if (hipDeviceSynchronize() != hipSuccess) return false;
+    if (hipMemcpy(dst, g_trace, n * 8, hipMemcpyDeviceToHost) != hipSuccess) return false;
+    return hipMemset(g_trace, 0, 2 * 4096 * 32 * 8) == hipSuccess;
+}
 #endif
 
 /* Copy the fp32 h of the last decode call, [64 unique experts][8 tokens]

@@ -31,6 +31,13 @@ bool ensure_pd(size_t floats);
 bool ensure_tickets(size_t n);
 bool ensure_xq(size_t elems);
 
+// route_k launch writing per-token lists (route.hip): row t at t*ostride,
+// plus expert `shared` with weight sg[t] (or 1) when shared >= 0, and the
+// per-token counts nh (optional).
+bool route_list_launch(const float *lg, int32_t *ids, float *wts, int32_t *nh, uint32_t n_tok,
+                       uint32_t n_exp, uint32_t topk, uint32_t ostride, int32_t shared,
+                       const float *sg);
+
 // Compute units of the current device (persistent grids size to it).
 int cu_count();
 

@@ -43,10 +43,17 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
 // different logits whose probabilities round to the same value (near-equal
 // logits, or probabilities that underflow to 0) go to the lower index.
 // Weights: p_i * (1/sum of the k picked p, in rank order).
+// Output row t of ids/wts starts at t * ostride (ostride >= topk).  With
+// shared >= 0 one more entry follows the topk picks: expert `shared` with
+// weight sg[t] (or 1 when sg is null), and nh[t] (when given) = topk + 1
+// (else topk): the per-token device lists of q4_hip_moe_exec_win /
+// q4_hip_moe_exec_dev.
 __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits, uint32_t n_tok,
                                                uint32_t n_exp, uint32_t topk,
                                                int32_t *__restrict__ ids,
-                                               float *__restrict__ wts) {
+                                               float *__restrict__ wts, uint32_t ostride,
+                                               int32_t shared, const float *__restrict__ sg,
+                                               int32_t *__restrict__ nh) {
     __shared__ int32_t s_id[4][64];
     __shared__ float s_p[4][64];
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -112,8 +119,15 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
     for (uint32_t k = 0; k < tk; k++) sk += s_p[w][k];
     const float inv2 = sk > 0.f ? __fdiv_rn(1.f, sk) : 0.f;
     for (uint32_t k = lane; k < topk; k += 64) {
-        ids[(size_t)t * topk + k] = k < tk ? s_id[w][k] : -1;
-        wts[(size_t)t * topk + k] = k < tk ? (sk > 0.f ? s_p[w][k] * inv2 : s_p[w][k]) : 0.f;
+        ids[(size_t)t * ostride + k] = k < tk ? s_id[w][k] : -1;
+        wts[(size_t)t * ostride + k] = k < tk ? (sk > 0.f ? s_p[w][k] * inv2 : s_p[w][k]) : 0.f;
+    }
+    if (lane == 0) {
+        if (shared >= 0) {
+            ids[(size_t)t * ostride + topk] = shared;
+            wts[(size_t)t * ostride + topk] = sg ? sg[t] : 1.f;
+        }
+        if (nh) nh[t] = (int32_t)(topk + (shared >= 0 ? 1u : 0u));
     }
 }
 
@@ -278,7 +292,15 @@ __global__ __launch_bounds__(256) void reduce_k(float *__restrict__ dy,
 bool route_launch(const float *lg, int32_t *ids, float *wts, uint32_t n_tok, uint32_t n_exp,
                   uint32_t topk) {
     route_k<<<dim3((n_tok + 3) / 4), dim3(256), 0, stream()>>>(lg, n_tok, n_exp, topk, ids,
-                                                              wts);
+                                                              wts, topk, -1, nullptr, nullptr);
+    return launch_ok("route_k");
+}
+
+bool route_list_launch(const float *lg, int32_t *ids, float *wts, int32_t *nh, uint32_t n_tok,
+                       uint32_t n_exp, uint32_t topk, uint32_t ostride, int32_t shared,
+                       const float *sg) {
+    route_k<<<dim3((n_tok + 3) / 4), dim3(256), 0, stream()>>>(lg, n_tok, n_exp, topk, ids,
+                                                              wts, ostride, shared, sg, nh);
     return launch_ok("route_k");
 }
 

@@ -1,0 +1,139 @@
+"""GPU parity for the router front q4mi_moe_route (router GEMV + shared-expert
+gate + softmax/top-k into per-token device lists) against the C oracle, and
+the layer it feeds (decode / verify window with the gated shared expert).
+
+Bars: logits bit-exact (the dot order is fixed: or_router restates it);
+routing ids bit-exact; routing weights and the gate <= 1e-6 relative (GPU
+exp vs the host's expf); layer outputs max rel error <= 1e-3.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+import oracle as om
+import q4mi
+from q4mi import synth
+
+pytestmark = pytest.mark.gpu
+T_IQ3_S = q4mi.T_IQ3_S
+TOL = 1e-3
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def zeros(shape, dtype=None):
+    import torch
+    return torch.zeros(shape, dtype=dtype or torch.float32, device="cuda")
+
+
+def router_rows(rng, ty, n_exp, K):
+    w = (rng.standard_normal((n_exp, K)) * 0.05).astype(np.float32)
+    if ty == 0:
+        return w
+    if ty == 1:
+        return w.astype(np.float16).view(np.uint8)
+    return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+
+
+def route(L, wr, ty, sgw, x, n_exp, topk, shared, ostride=64):
+    import torch
+    T, K = x.shape
+    lg = zeros((T, n_exp))
+    ids = torch.full((T, ostride), -7, dtype=torch.int32, device="cuda")
+    wts = zeros((T, ostride))
+    nh = zeros(T, torch.int32)
+    sg = zeros(T)
+    q4mi.check(L.q4mi_moe_route(q4mi.ptr(wr), ty, q4mi.ptr(sgw), q4mi.ptr(dev(x)), T, K, n_exp,
+                                topk, q4mi.ptr(lg), q4mi.ptr(ids), q4mi.ptr(wts), q4mi.ptr(nh),
+                                ostride, shared, q4mi.ptr(sg) if sgw is not None else None),
+               "q4mi_moe_route")
+    return host(lg), host(ids), host(wts), host(nh), host(sg)
+
+
+@pytest.mark.parametrize("ty,T,K,gate", [(0, 1, 2048, True), (0, 4, 2048, True),
+                                         (30, 4, 2048, False), (1, 37, 1024, True),
+                                         (0, 300, 4096, True), (30, 2048, 2048, True)])
+def test_route_front_matches_oracle(gpu, oracle, ty, T, K, gate):
+    rng = np.random.default_rng(ty * 100 + T + K)
+    n_exp, topk = 512, 10
+    w = router_rows(rng, ty, n_exp, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    g = (rng.standard_normal(K) * 0.02).astype(np.float32) if gate else None
+    lg, ids, wts, nh, sg = route(gpu, dev(w), ty, dev(g) if gate else None, x, n_exp, topk,
+                                 512)
+    res = oracle.router(ty, w, n_exp, K, x, sgw=g)
+    olg, osg = res if gate else (res, None)
+    assert np.array_equal(lg.view(np.uint32), olg.view(np.uint32))
+    oid, ow = oracle.softmax_topk(olg, topk)
+    assert np.array_equal(ids[:, :topk], oid)
+    assert np.allclose(wts[:, :topk], ow, rtol=1e-6, atol=1e-9)
+    # the shared expert's entry and the per-token counts
+    assert np.all(ids[:, topk] == 512) and np.all(nh == topk + 1)
+    if gate:
+        assert np.allclose(sg, osg, rtol=1e-6, atol=0)
+        assert np.allclose(wts[:, topk], osg, rtol=1e-6, atol=0)
+    else:
+        assert np.all(wts[:, topk] == 1.0)
+    assert np.all(ids[:, topk + 1:] == -7)     # nothing written past the row's entries
+
+
+def test_route_front_rejects(gpu):
+    import torch
+    x = zeros((1, 2048))
+    lg, ids, wts = zeros((1, 512)), zeros((1, 64), torch.int32), zeros((1, 64))
+    P = q4mi.ptr
+    assert not gpu.q4mi_moe_route(P(x), 2, None, P(x), 1, 2048, 512, 10, P(lg), P(ids), P(wts),
+                                  None, 64, -1, None)          # router type
+    assert not gpu.q4mi_moe_route(P(x), 0, None, P(x), 1, 2000, 512, 10, P(lg), P(ids), P(wts),
+                                  None, 64, -1, None)          # n_embd % 256
+    assert not gpu.q4mi_moe_route(P(x), 0, None, P(x), 1, 2048, 512, 10, P(lg), P(ids), P(wts),
+                                  None, 10, 512, None)         # ostride too small
+    assert not gpu.q4mi_moe_route(P(x), 0, P(x), P(x), 1, 2048, 512, 10, P(lg), P(ids), P(wts),
+                                  None, 64, 512, None)         # gate without d_sg
+
+
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_routed_layer_with_gated_shared_expert(gpu, oracle, n_tok):
+    """Router front -> device lists -> decode (1 token, q4_hip_moe_exec_dev)
+    or verify window (4 tokens): y = sum_k w_k FFN_k(x) + sg * FFN_shared(x)
+    against the oracle's layer with the oracle's routing and gate."""
+    from test_gpu_decode import layer
+    ly = layer()
+    H, F = ly.n_embd, ly.n_ff
+    rng = np.random.default_rng(60 + n_tok)
+    w = router_rows(rng, 0, 512, H)
+    g = (rng.standard_normal(H) * 0.02).astype(np.float32)
+    x = rng.standard_normal((n_tok, H)).astype(np.float32)
+    import torch
+    dx = dev(x)
+    lg, ids, wts, nh = zeros((n_tok, 512)), zeros((n_tok, 64), torch.int32), zeros((n_tok, 64)), \
+        zeros(n_tok, torch.int32)
+    sg = zeros(n_tok)
+    P = q4mi.ptr
+    q4mi.check(gpu.q4mi_moe_route(P(dev(w)), 0, P(dev(g)), P(dx), n_tok, H, 512, 10, P(lg),
+                                  P(ids), P(wts), P(nh), 64, 512, P(sg)), "route")
+    y = zeros((n_tok, H))
+    if n_tok == 1:
+        q4mi.check(gpu.q4_hip_moe_exec_dev(P(ly.d_arena), ly.stride, P(ids), P(wts), P(nh),
+                                           T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od, P(dx),
+                                           None, None, None, P(y), F, H, H), "exec_dev")
+    else:
+        q4mi.check(gpu.q4_hip_moe_exec_win(P(ly.d_arena), ly.stride, P(ids), P(wts), P(nh),
+                                           n_tok, T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od,
+                                           P(dx), None, P(y), F, H, H), "exec_win")
+    olg, osg = oracle.router(0, w, 512, H, x, sgw=g)
+    oid, ow = oracle.softmax_topk(olg, 10)
+    sid = np.concatenate([oid, np.full((n_tok, 1), 512, np.int32)], 1)
+    sw = np.concatenate([ow, osg[:, None]], 1).astype(np.float32)
+    yo = oracle.moe_tokens(H, F, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x, sid, sw)
+    assert rel_err(host(y), yo) <= TOL

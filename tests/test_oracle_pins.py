@@ -237,3 +237,71 @@ def test_dot8q_rows_is_dot8_of_quantized(oracle):
         a = oracle.dot8q_rows(ty, w, 40, K, q, d)
         b = oracle.dot8_rows(ty, w, 40, K, x)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _router_rows(rng, ty, n_exp, K):
+    w = (rng.standard_normal((n_exp, K)) * 0.05).astype(np.float32)
+    if ty == 0:
+        return w, w
+    if ty == 1:
+        h = w.astype(np.float16)
+        return h.view(np.uint8), h.astype(np.float32)
+    b = (w.view(np.uint32) >> 16).astype(np.uint16)      # BF16 by truncation
+    return b.view(np.uint8), (b.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("ty", [0, 1, 30])
+def test_router_logits_vs_reference_and_exact(oracle, ref, ty):
+    """or_router (the library's fixed dot order) against the reference's own
+    router GEMV q4_gemv (src/q4_quant.c:595-622, another order) and a
+    float64 dot: within 1e-5 of each row's sum of |w x|; and the routing the
+    reference takes from its logits equals the oracle's from its own."""
+    rng = np.random.default_rng(40 + ty)
+    n_exp, K, T = 512, 2048, 6
+    wb, wf = _router_rows(rng, ty, n_exp, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    lg = oracle.router(ty, wb, n_exp, K, x)
+    for t in range(T):
+        rl = ref.gemv(ty, wb, n_exp, K, x[t])
+        exact = wf.astype(np.float64) @ x[t].astype(np.float64)
+        scale = np.abs(wf.astype(np.float64)) @ np.abs(x[t].astype(np.float64))
+        assert np.all(np.abs(lg[t] - exact) <= 1e-5 * scale)
+        assert np.all(np.abs(rl - exact) <= 1e-5 * scale)
+        oid, _ = oracle.softmax_topk(lg[t], 10)
+        rid, _ = ref.softmax_topk(rl, 10)
+        assert np.array_equal(oid, rid)
+
+
+def test_router_dot_order_closed_form(oracle):
+    """The fixed order on inputs where every partial sum is exact (small
+    integers): the logits are the exact integer dots; and a single non-zero
+    product lands unchanged wherever it sits."""
+    rng = np.random.default_rng(9)
+    n_exp, K = 64, 512
+    w = rng.integers(-8, 9, (n_exp, K)).astype(np.float32)
+    x = rng.integers(-8, 9, (2, K)).astype(np.float32)
+    lg = oracle.router(0, w, n_exp, K, x)
+    assert np.array_equal(lg, (x.astype(np.int64) @ w.T.astype(np.int64)).astype(np.float32))
+    w1 = np.zeros((K, K), np.float32)
+    w1[np.arange(K), np.arange(K)] = 3.0
+    lg1 = oracle.router(0, w1, K, K, x[:1])
+    assert np.array_equal(lg1[0], 3.0 * x[0])
+
+
+def test_sgate_closed_form(oracle):
+    """sigmoid(sgw . x): a zero gate vector gives exactly 0.5, a large
+    positive dot gives 1, a large negative one 0; otherwise 1/(1+e^-d)."""
+    rng = np.random.default_rng(10)
+    K = 1024
+    w = np.zeros((4, K), np.float32)
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    _, sg = oracle.router(0, w, 4, K, x, sgw=np.zeros(K, np.float32))
+    assert np.all(sg == 0.5)
+    _, sg = oracle.router(0, w, 4, K, x, sgw=x[0] * 10)
+    assert sg[0] == 1.0
+    _, sg = oracle.router(0, w, 4, K, x, sgw=-x[0] * 10)
+    assert sg[0] == 0.0
+    g = (rng.standard_normal(K) * 0.01).astype(np.float32)
+    _, sg = oracle.router(0, w, 4, K, x, sgw=g)
+    d = x.astype(np.float64) @ g.astype(np.float64)
+    assert np.allclose(sg, 1 / (1 + np.exp(-d)), rtol=1e-6, atol=0)
