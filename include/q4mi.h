@@ -129,6 +129,20 @@ bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_
                          uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt, uint64_t od,
                          const float *d_x, float *d_h, float *d_y, uint32_t n_ff,
                          uint32_t in_dim, uint32_t n_embd);
+/* Decode (n_tok 1) or verify window (2..8) over the GGUF expert layout:
+ * gate, up and down are separate stacked tensors (blk.N.ffn_gate_exps,
+ * ffn_up_exps, ffn_down_exps), expert e's matrices at gate + e*gu_stride,
+ * up + e*gu_stride and down + e*d_stride (gate/up type gt, down type dt).
+ * Device lists and y as q4_hip_moe_exec_win.  The slices are the ones the
+ * reference's expert loader reads (q4_expert_parts, src/q4_expert.c:
+ * 962-982); a shared expert joins the lists once it is placed at index
+ * n_exp of the stacked tensors.  No reference counterpart (the reference
+ * packed experts into cache slots first). */
+bool q4mi_moe_exec_parts(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                         uint64_t gu_stride, uint64_t d_stride, const int32_t *d_es,
+                         const float *d_ew, const int32_t *d_nh, uint32_t n_tok, uint32_t gt,
+                         uint32_t dt, const float *d_x, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd);
 /* Per-token small batch: token t's picks at d_slots/d_wts[h_off[t] ..
  * h_off[t+1]) (device arrays, host prefix offsets), x and y token-major, y
  * accumulated; nothing is queued when false is returned.  Equal counts run
@@ -276,6 +290,17 @@ bool q4mi_mmq_mul_id_x(const void *w, const void *w_extra, uint32_t type, uint64
                        uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
                        const void *xq, const int32_t *bounds, uint64_t total_rows, float *dst,
                        uint64_t ld_dst);
+/* q4mi_mmq_gate_up over the GGUF expert layout: expert e's gate matrix at
+ * w_gate + e*expert_stride_bytes and its up matrix at w_up +
+ * e*expert_stride_bytes (separate stacked tensors); with wx_gate / wx_up
+ * (a shared expert's own tensors, both or neither) expert n_expert is that
+ * shared expert (bounds then has n_expert + 2 entries).  w_up must sit at
+ * the same offset within a dword as w_gate.  No reference counterpart. */
+bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type, uint64_t n_ff,
+                            uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                            const void *xq, uint64_t xrows, const int32_t *act_row,
+                            const int32_t *bounds, uint64_t total_rows, void *hq,
+                            const void *wx_gate, const void *wx_up);
 /* q4_hip_expert_reduce plus one extra row per token:
  * d_y[t] += sum_k rw*pd[rsrc] + xw[t]*pd[x_row0 + t] (d_xw NULL: weight 1;
  * the reference applies the shared expert's sigmoid gate there,

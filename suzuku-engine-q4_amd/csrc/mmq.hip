@@ -180,6 +180,8 @@ struct MmqLds {
 struct MmqArgs {
     const uint8_t *w;
     const uint8_t *wx;      // optional: base of expert ex (else w + ex * estride)
+    const uint8_t *wx_up;   // fused mode: expert ex's up rows (with wx)
+    uint64_t up_off;        // fused mode: expert e's up rows at w + e*estride + up_off
     uint32_t ex;
     uint64_t estride;       // bytes between experts
     uint32_t rb;            // bytes per weight row
@@ -304,14 +306,17 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     const uint32_t e = (uint32_t)tinfo.x;
     const int32_t rbase = tinfo.y;
     const uint32_t mrows = min((uint32_t)tinfo.z, 32u * NSUB);
-    const uint8_t *We = (a.wx && e == a.ex) ? a.wx : a.w + (uint64_t)e * a.estride;
-    // weight row (within the expert) of tile row r
+    const bool isx = a.wx && e == a.ex;
+    const uint8_t *We = isx ? a.wx : a.w + (uint64_t)e * a.estride;
+    // fused mode: the expert's up rows (after its gate rows in a packed
+    // expert; another tensor in the GGUF layout)
+    const uint8_t *Wu = isx ? a.wx_up : We + a.up_off;
+    // weight row (within the gate or up matrix) of tile row r
     const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
-    auto wrow = [&](uint32_t r) -> uint32_t {
-        return FUSED ? (r < 64 ? nblk + r : a.n_ff + nblk + (r - 64)) : nblk + r;
-    };
     auto wsrc = [&](uint32_t r, uint32_t sbi) -> const uint8_t * {
-        return We + (uint64_t)wrow(r) * a.rb + (uint64_t)sbi * SB;
+        const uint8_t *m = (FUSED && r >= 64) ? Wu : We;
+        const uint32_t wr = (FUSED && r >= 64) ? nblk + (r - 64) : nblk + r;
+        return m + (uint64_t)wr * a.rb + (uint64_t)sbi * SB;
     };
 
     // the codebook entries this thread converts (loaded now, stored into
@@ -673,7 +678,8 @@ static bool mmq_launch(const MmqArgs &a, dim3 grid) {
 bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, uint64_t estride,
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
              const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq,
-             const uint8_t *wx = nullptr) {
+             const uint8_t *wx = nullptr, const uint8_t *w_up = nullptr,
+             const uint8_t *wx_up = nullptr) {
     if (!total_rows) return true;
     // tile height: the largest of 128, 64, 32 rows whose block count (from
     // the whole-tile lower bound) still fills two blocks per CU.  Small
@@ -699,6 +705,9 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.ex = n_exp - 1;
     a.estride = estride;
     a.rb = (uint32_t)q4mi_row_bytes(ty, w_cols);
+    // packed experts: up rows follow the n_ff gate rows
+    a.up_off = w_up ? (uint64_t)(w_up - w) : (w_rows / 2) * a.rb;
+    a.wx_up = wx_up ? wx_up : (wx ? wx + (w_rows / 2) * a.rb : nullptr);
     a.K = (uint32_t)w_cols;
     a.n_ff = (uint32_t)(w_rows / 2);
     a.xq = (const _Float16 *)xq;
@@ -885,6 +894,39 @@ bool q4mi_mmq_mul_id_x(const void *w, const void *w_extra, uint32_t type, uint64
     return mmq_run((const uint8_t *)w, type, w_rows, w_cols, expert_stride_bytes, n_expert + 1, xq,
                    total_rows, nullptr, bounds, total_rows, dst, ld_dst, nullptr,
                    (const uint8_t *)w_extra);
+}
+
+/* q4mi_mmq_gate_up over the GGUF expert layout: gate and up are separate
+ * stacked tensors (blk.N.ffn_gate_exps / ffn_up_exps), expert e's gate
+ * matrix at w_gate + e*expert_stride and its up matrix at w_up +
+ * e*expert_stride; with wx_gate / wx_up (a shared expert's own 2-D
+ * tensors), expert n_expert is that shared expert over bounds[n_expert] ..
+ * bounds[n_expert + 1].  The up base must sit at the same offset within a
+ * dword as the gate base. */
+bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type, uint64_t n_ff,
+                            uint64_t w_cols, uint64_t expert_stride_bytes, uint32_t n_expert,
+                            const void *xq, uint64_t xrows, const int32_t *act_row,
+                            const int32_t *bounds, uint64_t total_rows, void *hq,
+                            const void *wx_gate, const void *wx_up) {
+    if (!w_gate || !w_up || !xq || !bounds || !hq || !n_expert || n_expert > 1023 || !w_cols ||
+        !xrows || ((uintptr_t)hq & 15) || ((uintptr_t)xq & 15) || n_ff % 64 ||
+        (!wx_gate) != (!wx_up)) {
+        set_error("q4mi_mmq_gate_up_parts: bad arguments");
+        return false;
+    }
+    if (((uintptr_t)w_gate ^ (uintptr_t)w_up) & 3u ||
+        (wx_gate && (((uintptr_t)wx_gate ^ (uintptr_t)wx_up) & 3u))) {
+        set_error("q4mi_mmq_gate_up_parts: up base at another in-dword offset than gate");
+        return false;
+    }
+    if (!mmq_supported(type, 2 * n_ff, w_cols)) {
+        set_error("q4mi_mmq_gate_up_parts: type/shape not covered");
+        return false;
+    }
+    return mmq_run((const uint8_t *)w_gate, type, 2 * n_ff, w_cols, expert_stride_bytes,
+                   n_expert + (wx_gate ? 1u : 0u), xq, xrows, act_row, bounds, total_rows,
+                   nullptr, 0, hq, (const uint8_t *)wx_gate, (const uint8_t *)w_up,
+                   (const uint8_t *)wx_up);
 }
 
 /* h[r][k] = silu(gu[r][k]) * gu[r][n_ff + k]. */

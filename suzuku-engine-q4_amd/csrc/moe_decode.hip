@@ -331,6 +331,7 @@ __device__ inline void group_w(const uint32_t *stab, const uint8_t *lb, const ui
 struct MoeArgs {
     const uint8_t *base;
     uint64_t stride, og, ou, od;
+    uint64_t stride_d;  // bytes between experts' down matrices (= stride when packed)
     uint32_t K;       // in_dim (gate/up columns)
     uint32_t n_ff;
     uint32_t n_embd;
@@ -763,7 +764,7 @@ __device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
                                   uint32_t S, int32_t idv, uint32_t nu, uint32_t r0, uint32_t nr,
                                   uint32_t wave, uint32_t lane) {
     const uint8_t *base = a.base;
-    const uint64_t stride = a.stride, od = a.od;
+    const uint64_t stride = a.stride_d, od = a.od;
     const uint32_t rb = a.rb_dn, slot_bytes = ch * kDnRows * rb;
     const uint32_t C = (nu + ch - 1) / ch;
     uint32_t issued = 0;
@@ -1115,7 +1116,7 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
     a.slots = S;
     // a block copies one contiguous run of kDnRows rows per expert: 16-byte
     // units need that run (not each row) 16-byte aligned and sized
-    const bool wide = ((((uintptr_t)a.base) | a.stride | a.od | ((uint64_t)kDnRows * a.rb_dn)) & 15u) == 0 &&
+    const bool wide = ((((uintptr_t)a.base) | a.stride_d | a.od | ((uint64_t)kDnRows * a.rb_dn)) & 15u) == 0 &&
                       a.n_embd % kDnRows == 0;
     const void *fn = wide ? (const void *)moe_dn_k<TY, NT, TPR, GPT, 16>
                           : (const void *)moe_dn_k<TY, NT, TPR, GPT, 4>;
@@ -1226,7 +1227,8 @@ struct Work {
 static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
                     const HostList &hl, uint32_t nu_host, uint32_t gt, uint64_t og, uint32_t ut,
                     uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_y,
-                    uint32_t n_ff, uint32_t in_dim, uint32_t n_embd, Work work = Work{}) {
+                    uint32_t n_ff, uint32_t in_dim, uint32_t n_embd, Work work = Work{},
+                    uint64_t stride_d = 0) {
     if (!base || !d_x || !d_y || src.n_tok < 1 || src.n_tok > kMaxT) {
         set_error("moe: bad arguments");
         return false;
@@ -1244,7 +1246,8 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
         set_error("moe: y must be 4-byte aligned");
         return false;
     }
-    if ((((uintptr_t)base) | stride | og | ou | od) & 3u) {
+    if (!stride_d) stride_d = stride;
+    if ((((uintptr_t)base) | stride | stride_d | og | ou | od) & 3u) {
         set_error("moe: expert arena offsets must be 4-byte aligned");
         return false;
     }
@@ -1252,6 +1255,7 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     MoeArgs a = {};
     a.base = base;
     a.stride = stride;
+    a.stride_d = stride_d;
     a.og = og;
     a.ou = ou;
     a.od = od;
@@ -1544,6 +1548,28 @@ bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_
     ListSrc src = {d_es, d_ew, d_nh, kMaxU, n_tok, 0, 0};
     return moe_run(base, stride, src, hl, 0, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
                    n_embd);
+}
+
+/* Decode (1 token) or verify window (2..8) over the GGUF expert layout:
+ * gate, up and down are separate stacked tensors (blk.N.ffn_gate_exps,
+ * ffn_up_exps, ffn_down_exps; src/q4_expert.c:962-982 reads the same
+ * slices), expert e's matrices at gate + e*gu_stride, up + e*gu_stride and
+ * down + e*d_stride.  Device lists as q4_hip_moe_exec_win. */
+bool q4mi_moe_exec_parts(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                         uint64_t gu_stride, uint64_t d_stride, const int32_t *d_es,
+                         const float *d_ew, const int32_t *d_nh, uint32_t n_tok, uint32_t gt,
+                         uint32_t dt, const float *d_x, float *d_y, uint32_t n_ff,
+                         uint32_t in_dim, uint32_t n_embd) {
+    if (!gate || !up || !down || !d_es || !d_ew || !d_nh || !n_tok || n_tok > kMaxT ||
+        !gu_stride || !d_stride) {
+        set_error("q4mi_moe_exec_parts: bad arguments");
+        return false;
+    }
+    HostList hl = {};
+    ListSrc src = {d_es, d_ew, d_nh, kMaxU, n_tok, 0, 0};
+    // offsets from the gate base wrap modulo 2^64, so up/down may sit below it
+    return moe_run(gate, gu_stride, src, hl, 0, gt, 0, gt, (uint64_t)(up - gate), dt,
+                   (uint64_t)(down - gate), d_x, d_y, n_ff, in_dim, n_embd, Work{}, d_stride);
 }
 
 /* Per-token small-batch preflight: the type/shape rule of the exec calls. */

@@ -60,6 +60,8 @@ _SIGS = {
     "q4_hip_moe_win_ok": (_b, [_u32, _u32, _u32, _u32, _u32, _u32]),
     "q4_hip_moe_exec_win": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
                                  _u64, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4mi_moe_exec_parts": (_b, [_vp, _vp, _vp, _u64, _u64, _vp, _vp, _vp, _u32, _u32, _u32,
+                                 _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_moe_tok_ok": (_b, [_u32, _u32, _u32, _u32, _u32]),
     "q4_hip_moe_exec_tok": (_b, [_vp, _u64, _vp, _vp, _vp, _u32, _u32, _u64, _u32, _u64, _u32,
                                  _u64, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
@@ -94,6 +96,8 @@ _SIGS = {
                                 _u64, _vp]),
     "q4mi_mmq_mul_id_x": (_b, [_vp, _vp, _u32, _u64, _u64, _u64, _u32, _vp, _vp, _u64, _vp,
                                _u64]),
+    "q4mi_mmq_gate_up_parts": (_b, [_vp, _vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp,
+                                    _vp, _u64, _vp, _vp, _vp]),
     "q4mi_expert_reduce_x": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u64, _vp]),
 }
 
