@@ -15,7 +15,11 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 T_Q8_0 = 8
+T_Q6_K = 14
+T_IQ4_NL = 20
 T_IQ3_S = 21
+T_IQ2_S = 22
+T_Q2_0 = 42
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -28,12 +32,15 @@ def _p(a, t):
     return a.ctypes.data_as(t)
 
 
+_BLOCK = {T_IQ3_S: (256, 110), T_Q8_0: (32, 34), T_IQ4_NL: (32, 18), T_Q2_0: (64, 18),
+          T_IQ2_S: (256, 82), T_Q6_K: (256, 210)}
+
+
 def row_bytes(ty, n):
-    if ty == T_IQ3_S:
-        return n // 256 * 110
-    if ty == T_Q8_0:
-        return n // 32 * 34
-    raise ValueError(ty)
+    if ty not in _BLOCK:
+        raise ValueError(ty)
+    vals, nb = _BLOCK[ty]
+    return n // vals * nb
 
 
 class Oracle:
@@ -183,6 +190,8 @@ class Ref:
                                                            ctypes.c_uint32, _i32p, _f32p,
                                                            _u32p, _f32p]
         L.qref_softmax_topk.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _f32p]
+        L.q4_dequant_row.restype = ctypes.c_bool
+        L.q4_dequant_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p]
         L.q4_gemv.restype = ctypes.c_bool
         L.q4_gemv.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
                               _f32p, ctypes.c_float]
@@ -225,6 +234,13 @@ class Ref:
         assert self.L.qref_moe_win(n_embd, n_ff, t_gu, t_d, n_exp, _p(arena, _u8p), stride,
                                    _p(x, _f32p), n_tok, _p(ids, _i32p), _p(wts, _f32p),
                                    _p(tn, _u32p), _p(y, _f32p))
+        return y
+
+    def dequant_row(self, ty, w, n):
+        """The reference's float dequantizer (q4_dequant_row)."""
+        w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+        y = np.empty(n, np.float32)
+        assert self.L.q4_dequant_row(ty, _p(w, _u8p), n, _p(y, _f32p))
         return y
 
     def gemv(self, ty, w, rows, cols, x):

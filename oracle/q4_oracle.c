@@ -35,10 +35,19 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "../include/q4mi_iq2s_grid.h"
 #include "../include/q4mi_iq3s_grid.h"
 
 #define OR_T_Q8_0 8u
+#define OR_T_Q6_K 14u
+#define OR_T_IQ4_NL 20u
 #define OR_T_IQ3_S 21u
+#define OR_T_IQ2_S 22u
+#define OR_T_Q2_0 42u
+
+/* IQ4_NL value table (the format's, src/q4_quant.c:13-15) */
+static const int8_t or_kv_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                       1,    13,   25,  38,  53,  69,  89,  113};
 
 float or_f16_to_f32(uint16_t h) {
     uint32_t s = ((uint32_t)h & 0x8000u) << 16;
@@ -68,9 +77,72 @@ float or_f16_to_f32(uint16_t h) {
 }
 
 uint64_t or_row_bytes(uint32_t type, uint64_t n) {
-    if (type == OR_T_IQ3_S) return n % 256 ? 0 : n / 256 * 110;
-    if (type == OR_T_Q8_0) return n % 32 ? 0 : n / 32 * 34;
+    switch (type) {
+    case OR_T_IQ3_S: return n % 256 ? 0 : n / 256 * 110;
+    case OR_T_Q8_0: return n % 32 ? 0 : n / 32 * 34;
+    case OR_T_IQ4_NL: return n % 32 ? 0 : n / 32 * 18;
+    case OR_T_Q2_0: return n % 64 ? 0 : n / 64 * 18;
+    case OR_T_IQ2_S: return n % 256 ? 0 : n / 256 * 82;
+    case OR_T_Q6_K: return n % 256 ? 0 : n / 256 * 210;
+    }
     return 0;
+}
+
+static float or_h2f_at(const uint8_t *p) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return or_f16_to_f32(h);
+}
+
+/* Integers of one 32-value group of the non-IQ3_S formats: wi = the signed
+ * integer weights, lm[l] = the integer multiplier of values 4l..4l+3, *d =
+ * the float block scale (IQ2_S: d * 0.125).  Follows the reference's
+ * dequantizers (src/q4_quant.c: Q2_0 :177-188, IQ4_NL :273-288, IQ2_S
+ * :290-322, Q6_K :481-510), whose float value of element i is
+ * *d * lm[i/4] * wi[i]. */
+static void or_group_other(uint32_t type, const uint8_t *w, uint64_t g, int32_t wi[32],
+                           int32_t lm[8], float *d) {
+    for (int l = 0; l < 8; l++) lm[l] = 1;
+    if (type == OR_T_IQ4_NL) {
+        const uint8_t *blk = w + 18 * g;
+        *d = or_h2f_at(blk);
+        for (int j = 0; j < 16; j++) {
+            wi[j] = or_kv_iq4nl[blk[2 + j] & 15];
+            wi[j + 16] = or_kv_iq4nl[blk[2 + j] >> 4];
+        }
+    } else if (type == OR_T_Q2_0) {
+        const uint8_t *blk = w + 18 * (g / 2);
+        *d = or_h2f_at(blk);
+        const uint8_t *qs = blk + 2 + 8 * (g % 2);
+        for (int j = 0; j < 32; j++) wi[j] = (int32_t)((qs[j / 4] >> (2 * (j % 4))) & 3) - 1;
+    } else if (type == OR_T_IQ2_S) {
+        const uint8_t *blk = w + 82 * (g / 8);
+        const int ib = (int)(g % 8);
+        *d = or_h2f_at(blk) * 0.125f;
+        const uint8_t *qs = blk + 2 + 4 * ib, *sg = blk + 34 + 4 * ib;
+        const uint32_t qh = blk[66 + ib], sc = blk[74 + ib];
+        for (int l = 0; l < 4; l++) {
+            const uint64_t e = q4mi_iq2s_entry(qs[l] | ((qh << (8 - 2 * l)) & 0x300));
+            for (int j = 0; j < 8; j++) {
+                const int mag = (int)((e >> (8 * j)) & 0xff);
+                wi[8 * l + j] = ((sg[l] >> j) & 1) ? -mag : mag;
+            }
+        }
+        for (int l = 0; l < 8; l++) lm[l] = 2 * (int32_t)(l < 4 ? (sc & 15) : (sc >> 4)) + 1;
+    } else { /* Q6_K: group g = 32 values of a 256-value superblock */
+        const uint8_t *blk = w + 210 * (g / 8);
+        const int j = (int)(g % 8), h = j / 4, gq = j % 4;
+        *d = or_h2f_at(blk + 208);
+        const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+        const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+        for (int l = 0; l < 32; l++) {
+            const int lo = (gq & 1) ? ql[l + 32] : ql[l];
+            const int q4 = (gq & 2) ? (lo >> 4) : (lo & 15);
+            const int q2 = (qh[l] >> (2 * gq)) & 3;
+            wi[l] = (q4 | (q2 << 4)) - 32;
+        }
+        for (int l = 0; l < 8; l++) lm[l] = sc[2 * gq + (l < 4 ? 0 : 1)];
+    }
 }
 
 /* _mm256_cvtps_epi32 under the default MXCSR: round to nearest even; a value
@@ -119,7 +191,28 @@ int or_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *y) {
         }
         return 1;
     }
-    if (type != OR_T_IQ3_S || n % 256) return 0;
+    if (type != OR_T_IQ3_S) {
+        if (!or_row_bytes(type, n)) return 0;
+        int32_t wi[32], lm[8];
+        float d;
+        for (uint64_t g = 0; g < n / 32; g++) {
+            or_group_other(type, w, g, wi, lm, &d);
+            for (int i = 0; i < 32; i++) {
+                /* the reference's float expression per format */
+                float v;
+                if (type == OR_T_IQ2_S)   /* dl = d * (0.5 + s) * 0.25 */
+                    v = (or_h2f_at(w + 82 * (g / 8)) * (0.5f + (float)((lm[i / 4] - 1) / 2)) *
+                         0.25f) * (float)wi[i];
+                else if (type == OR_T_Q6_K) /* d * sc * (q - 32) */
+                    v = d * (float)lm[i / 4] * (float)wi[i];
+                else
+                    v = d * (float)wi[i];
+                y[32 * g + i] = v;
+            }
+        }
+        return 1;
+    }
+    if (n % 256) return 0;
     for (uint64_t b = 0; b < n / 256; b++) {
         const uint8_t *blk = w + 110 * b;
         uint16_t dh;
@@ -178,12 +271,25 @@ static void or_group_ints(uint32_t type, const uint8_t *w, uint64_t g,
     }
 }
 
-/* Exact per-group sums S_g = mult_g * sum_i w_i q_i (int32). */
+static int or_other(uint32_t type) {
+    return type == OR_T_IQ4_NL || type == OR_T_Q2_0 || type == OR_T_IQ2_S || type == OR_T_Q6_K;
+}
+
+/* Exact per-group sums S_g = sum_l lm_l * sum_{i in quad l} w_i q_i (int32;
+ * IQ3_S / Q8_0: one multiplier per group). */
 int or_group_sums(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
                   int32_t *s) {
     if (!or_row_bytes(type, n)) return 0;
-    int32_t wi[32], mult;
+    int32_t wi[32], mult, lm[8];
+    float d;
     for (uint64_t g = 0; g < n / 32; g++) {
+        if (or_other(type)) {
+            or_group_other(type, w, g, wi, lm, &d);
+            int32_t acc = 0;
+            for (int i = 0; i < 32; i++) acc += lm[i / 4] * wi[i] * (int32_t)q[32 * g + i];
+            s[g] = acc;
+            continue;
+        }
         or_group_ints(type, w, g, wi, &mult);
         int32_t acc = 0;
         for (int i = 0; i < 32; i++) acc += wi[i] * (int32_t)q[32 * g + i];
@@ -199,7 +305,35 @@ int or_group_sums(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
 float or_dot8(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
               const float *dx) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int32_t wi[32], mult;
+    int32_t wi[32], mult, lm[8];
+    if (or_other(type)) {
+        /* IQ4_NL, IQ2_S (dq8_iq4_nl / dq8_iq2_s, src/q4_cpuexp.c:814-853,
+         * :978-1005): lane l gets fma(d*d_x, lm_l * sum of quad l, .);
+         * Q2_0 (dq8_q2_0 :1113-1150): lanes take the unsigned codes
+         * (w + 1) and a serial cs = fma(d*d_x, sum(q), cs) is subtracted after the
+         * fold.  Q6_K (no CPU expert kernel in the reference) uses the
+         * IQ4_NL structure with its int8 sub-block scales. */
+        float cs = 0.f, d;
+        for (uint64_t g = 0; g < n / 32; g++) {
+            or_group_other(type, w, g, wi, lm, &d);
+            const float dd = d * dx[g];
+            int32_t bs = 0;
+            for (int l = 0; l < 8; l++) {
+                int32_t li = 0;
+                for (int b = 0; b < 4; b++) {
+                    const int32_t v = type == OR_T_Q2_0 ? wi[4 * l + b] + 1 : wi[4 * l + b];
+                    li += v * (int32_t)q[32 * g + 4 * l + b];
+                    bs += q[32 * g + 4 * l + b];
+                }
+                acc[l] = fmaf(dd, (float)(li * lm[l]), acc[l]);
+            }
+            /* the reference is built with FMA contraction (gcc -O3 -mfma) */
+            if (type == OR_T_Q2_0) cs = fmaf(dd, (float)bs, cs);
+        }
+        const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+        const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+        return ((l0 + l2) + (l1 + l3)) - cs;
+    }
     for (uint64_t g = 0; g < n / 32; g++) {
         or_group_ints(type, w, g, wi, &mult);
         uint16_t dh;

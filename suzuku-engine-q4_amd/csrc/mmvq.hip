@@ -1,5 +1,5 @@
 // Dense decode MMVQ: y[t][r] = scale * (W_r . q8(x_t)) for 1..8 tokens over
-// IQ3_S or Q8_0 weight rows.  C ABI: q4_mmvq_n and friends (reference
+// IQ3_S, Q8_0, IQ4_NL, Q2_0, IQ2_S or Q6_K weight rows.  C ABI: q4_mmvq_n and friends (reference
 // src/q4_mmvq.cu:266-349, src/q4.h:914-927) plus q4mi_mmvq, which takes
 // already-quantized activations and can export the per-group int32 sums.
 #include <stdlib.h>
@@ -24,13 +24,13 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
                                               float *__restrict__ y, float scale,
                                               int32_t *__restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
-    Iq3sLds *tab = (Iq3sLds *)smem;
-    uint8_t *tile = smem + (F::kTables ? sizeof(Iq3sLds) : 0);
+    void *tab = smem;
+    uint8_t *tile = smem + F::kTabBytes;
     const uint32_t tid = threadIdx.x;
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nr = min(R, rows - r0);
     const uint32_t G = K / 32;
-    if (F::kTables) q4mi_iq3s_tables_init(tab, tid, 256);
+    F::init(tab, tid, 256);
     stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
@@ -72,7 +72,9 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
 }
 
 // weight bytes per row tile
-static uint32_t tile_target(uint32_t ty) { return ty == Q4MI_T_Q8_0 ? 24576u : 14336u; }
+static uint32_t tile_target(uint32_t ty) {
+    return ty == Q4MI_T_Q8_0 || ty == Q4MI_T_Q6_K ? 24576u : 14336u;
+}
 
 template <class F, int NT>
 static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const float *xf,
@@ -84,7 +86,7 @@ static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const fl
     const uint32_t target = tile_target(F::kType);
     const uint32_t R = tile_rows(rb, L.tpr, target);
     const size_t xlds = xf ? (size_t)NT * K + (size_t)NT * (K / 32) * 4 : 0;
-    const size_t lds = (F::kTables ? sizeof(Iq3sLds) : 0) + (((size_t)R * rb + 15) & ~(size_t)15) +
+    const size_t lds = F::kTabBytes + (((size_t)R * rb + 15) & ~(size_t)15) +
                        xlds + 64;
     const dim3 grid((rows + R - 1) / R), blk(256);
 #define Q4MI_L(T, P)                                                                     \
@@ -109,19 +111,38 @@ static bool mmvq_launch(const uint8_t *W, uint32_t rows, uint32_t K, const float
     return mmvq_launch_nt<F, 8>(W, rows, K, xf, xq, xd, nt, y, scale, sums);
 }
 
+// IQ3_S, Q8_0, IQ4_NL, Q2_0, IQ2_S, Q6_K with 8..256 groups per row (a
+// whole number of blocks).
 bool mmvq_covered(uint32_t ty, uint64_t K) {
-    if (ty != Q4MI_T_IQ3_S && ty != Q4MI_T_Q8_0) return false;
+    switch (ty) {
+    case Q4MI_T_IQ3_S: case Q4MI_T_Q8_0: case Q4MI_T_IQ4_NL: case Q4MI_T_Q2_0:
+    case Q4MI_T_IQ2_S: case Q4MI_T_Q6_K: break;
+    default: return false;
+    }
     if (!q4mi_row_bytes(ty, K) || K > 8192) return false;
     return layout_for((uint32_t)(K / 32)).tpr != 0;
 }
 
+// one launch for the type: pre-quantized (xq, xd) or fp32 x (xf)
+static bool mmvq_any(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const float *xf,
+                     const int8_t *xq, const float *xd, uint32_t nt, float *y, float scale,
+                     int32_t *sums) {
+    const uint32_t r = (uint32_t)rows, k = (uint32_t)K;
+    switch (ty) {
+    case Q4MI_T_IQ3_S: return mmvq_launch<FmtIQ3S>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    case Q4MI_T_Q8_0: return mmvq_launch<FmtQ80>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    case Q4MI_T_IQ4_NL: return mmvq_launch<FmtIQ4NL>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    case Q4MI_T_Q2_0: return mmvq_launch<FmtQ20>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    case Q4MI_T_IQ2_S: return mmvq_launch<FmtIQ2S>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    case Q4MI_T_Q6_K: return mmvq_launch<FmtQ6K>(W, r, k, xf, xq, xd, nt, y, scale, sums);
+    }
+    set_error("mmvq: type %u not covered", ty);
+    return false;
+}
+
 bool mmvq_q8(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const int8_t *xq,
              const float *xd, uint32_t nt, float *y, float scale, int32_t *sums) {
-    if (ty == Q4MI_T_IQ3_S)
-        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, nullptr, xq, xd, nt, y,
-                                    scale, sums);
-    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, nullptr, xq, xd, nt, y, scale,
-                               sums);
+    return mmvq_any(ty, W, rows, K, nullptr, xq, xd, nt, y, scale, sums);
 }
 
 // Activations quantized inside the GEMV blocks: used while the codes of the
@@ -141,11 +162,7 @@ static bool mmvq_fused_fits(uint32_t ty, uint64_t rows, uint64_t K, uint32_t nt)
 
 static bool mmvq_f32(uint32_t ty, const uint8_t *W, uint64_t rows, uint64_t K, const float *x,
                      uint32_t nt, float *y, float scale) {
-    if (ty == Q4MI_T_IQ3_S)
-        return mmvq_launch<FmtIQ3S>(W, (uint32_t)rows, (uint32_t)K, x, nullptr, nullptr, nt, y,
-                                    scale, nullptr);
-    return mmvq_launch<FmtQ80>(W, (uint32_t)rows, (uint32_t)K, x, nullptr, nullptr, nt, y, scale,
-                               nullptr);
+    return mmvq_any(ty, W, rows, K, x, nullptr, nullptr, nt, y, scale, nullptr);
 }
 
 static int g_on = -1;

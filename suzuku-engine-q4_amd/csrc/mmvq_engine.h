@@ -11,29 +11,44 @@
 // float(S) * (d_w * d_x).  A DPP reduction over the TPR lanes finishes
 // the row.
 #pragma once
+#include "formats.h"
 #include "q4mi_common.h"
 
 namespace q4mi {
 
+// Formats of the engine: kType, kTabBytes (LDS tables before the tile),
+// kTwo (two multipliers per group, quads 0-3 and 4-7), init (build the
+// tables), decode (one 32-value group of a row in LDS, formats.h's WGroup).
 struct FmtIQ3S {
     static constexpr uint32_t kType = Q4MI_T_IQ3_S;
-    static constexpr bool kTables = true;
-    __device__ static inline void decode(const Iq3sLds *tab, const uint8_t *lb,
+    static constexpr uint32_t kTabBytes = sizeof(Iq3sLds);
+    static constexpr bool kTwo = false;
+    __device__ static inline void init(void *tab, uint32_t tid, uint32_t n) {
+        q4mi_iq3s_tables_init((Iq3sLds *)tab, (int)tid, (int)n);
+    }
+    __device__ static inline void decode(const void *tab, const uint8_t *lb,
                                          const uint32_t *lw, uint32_t row, uint32_t g,
-                                         Iq3sGroup &o) {
-        q4mi_iq3s_decode(tab, lb, lw, row, g, o);
+                                         WGroup &o) {
+        Iq3sGroup q;
+        q4mi_iq3s_decode((const Iq3sLds *)tab, lb, lw, row, g, q);
+#pragma unroll
+        for (int k = 0; k < 8; k++) o.w[k] = q.w[k];
+        o.m1 = o.m2 = q.mult;
+        o.d = q.d;
     }
 };
 
 struct FmtQ80 {
     static constexpr uint32_t kType = Q4MI_T_Q8_0;
-    static constexpr bool kTables = false;
-    __device__ static inline void decode(const Iq3sLds *, const uint8_t *lb,
+    static constexpr uint32_t kTabBytes = 0;
+    static constexpr bool kTwo = false;
+    __device__ static inline void init(void *, uint32_t, uint32_t) {}
+    __device__ static inline void decode(const void *, const uint8_t *lb,
                                          const uint32_t *lw, uint32_t row, uint32_t g,
-                                         Iq3sGroup &o) {
+                                         WGroup &o) {
         const uint32_t B = row + g * Q80_BYTES;
         o.d = q4mi_h2f(lds_u16_at(lb, B));
-        o.mult = 1;
+        o.m1 = o.m2 = 1;
         const uint32_t i0 = (B + 2u) >> 2, sh = (B + 2u) & 3u;
         uint32_t prev = lw[i0];
 #pragma unroll
@@ -44,6 +59,24 @@ struct FmtQ80 {
         }
     }
 };
+
+// Exact group sum against one token's eight activation quads.
+template <class F>
+__device__ inline int group_sum(const WGroup &w, const int32_t (&q)[8]) {
+    if constexpr (F::kTwo) {
+        int a = 0, b = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) a = q4mi_sdot4(w.w[k], q[k], a);
+#pragma unroll
+        for (int k = 4; k < 8; k++) b = q4mi_sdot4(w.w[k], q[k], b);
+        return a * w.m1 + b * w.m2;
+    } else {
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s = q4mi_sdot4(w.w[k], q[k], s);
+        return s * w.m1;
+    }
+}
 
 // q8 activations of this lane's GPT groups for NT tokens.
 template <int NT, int GPT>
@@ -80,20 +113,17 @@ __device__ inline void load_xregs(XRegs<NT, GPT> &x, const int8_t *xq, const flo
 // Partial dot of one row (this lane's groups) for NT tokens, added to acc.
 // sums (optional): per-token int32 group sums, sums[t * sum_tstride + g].
 template <class F, int NT, int GPT, int TPR>
-__device__ inline void row_dot(const Iq3sLds *tab, const uint8_t *lb, const uint32_t *lw,
+__device__ inline void row_dot(const void *tab, const uint8_t *lb, const uint32_t *lw,
                                uint32_t row, uint32_t gi, const XRegs<NT, GPT> &x,
                                float (&acc)[NT], int32_t *sums, size_t sum_tstride) {
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
         const uint32_t g = gi + TPR * m;
-        Iq3sGroup w;
+        WGroup w;
         F::decode(tab, lb, lw, row, g, w);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            int s = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) s = q4mi_sdot4(w.w[k], x.q[m][t][k], s);
-            s *= w.mult;
+            const int s = group_sum<F>(w, x.q[m][t]);
             acc[t] = fmaf((float)s, w.d * x.d[m][t], acc[t]);
             if (sums) sums[(size_t)t * sum_tstride + g] = s;
         }

@@ -20,9 +20,18 @@
 // Q8_0 block: fp16 d + int8 qs[32] (reference src/q4_quant.c:131-140)
 #define Q80_BYTES 34u
 
+// Row bytes of every format this library reads (0: not covered).  Besides
+// IQ3_S and Q8_0: Q6_K (14), IQ4_NL (20), IQ2_S (22), Q2_0 (42), whose
+// decoders are in formats.h.
 __host__ __device__ inline uint64_t q4mi_row_bytes(uint32_t ty, uint64_t n) {
-    if (ty == Q4MI_T_IQ3_S) return (n % 256) ? 0 : n / 256 * IQ3S_BYTES;
-    if (ty == Q4MI_T_Q8_0) return (n % 32) ? 0 : n / 32 * Q80_BYTES;
+    switch (ty) {
+    case Q4MI_T_IQ3_S: return (n % 256) ? 0 : n / 256 * IQ3S_BYTES;
+    case Q4MI_T_Q8_0: return (n % 32) ? 0 : n / 32 * Q80_BYTES;
+    case 14u: return n % 256 ? 0 : n / 256 * 210;   // Q6_K
+    case 20u: return n % 32 ? 0 : n / 32 * 18;      // IQ4_NL
+    case 22u: return n % 256 ? 0 : n / 256 * 82;    // IQ2_S
+    case 42u: return n % 64 ? 0 : n / 64 * 18;      // Q2_0
+    }
     return 0;
 }
 

@@ -32,10 +32,29 @@ def q80_bytes(rng, nblocks):
     return b.reshape(-1)
 
 
+T_Q6_K, T_IQ4_NL, T_IQ2_S, T_Q2_0 = 14, 20, 22, 42
+# (values per block, bytes per block, offset of the fp16 scale)
+BLOCKS = {T_IQ3_S: (256, 110, 0), T_Q8_0: (32, 34, 0), T_IQ4_NL: (32, 18, 0),
+          T_Q2_0: (64, 18, 0), T_IQ2_S: (256, 82, 0), T_Q6_K: (256, 210, 208)}
+
+
+def blocks_bytes(rng, ty, nblocks):
+    """Uniform bytes with an fp16 |N(0,1)| * 0.02 block scale: every field of
+    these formats (indices, signs, sub-block scales, quants) is then uniform
+    over its range."""
+    vals, nb, doff = BLOCKS[ty]
+    b = rng.integers(0, 256, size=(nblocks, nb), dtype=np.uint8)
+    d = (np.abs(rng.standard_normal(nblocks)) * 0.02).astype(np.float16)
+    b[:, doff:doff + 2] = d.view(np.uint8).reshape(nblocks, 2)
+    return b.reshape(-1)
+
+
 def matrix(rng, ty, rows, cols):
     if ty == T_IQ3_S:
         return iq3s_bytes(rng, rows * cols // 256)
-    return q80_bytes(rng, rows * cols // 32)
+    if ty == T_Q8_0:
+        return q80_bytes(rng, rows * cols // 32)
+    return blocks_bytes(rng, ty, rows * cols // BLOCKS[ty][0])
 
 
 def expert_stride(n_embd, n_ff, ty=T_IQ3_S):

@@ -1,0 +1,138 @@
+"""GPU parity for the weight formats beside IQ3_S / Q8_0 (IQ4_NL, Q2_0,
+IQ2_S, Q6_K), through the C ABI, against the C oracle (whose decoders and
+int8 dots are pinned bit for bit against the reference's CPU code in
+tests/test_oracle_formats.py).
+
+Bars: int32 group sums bit-exact; fp32 outputs max rel error <= 1e-3."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+import oracle as om
+import q4mi
+from q4mi import synth
+
+pytestmark = pytest.mark.gpu
+T_IQ3_S, T_Q8_0 = q4mi.T_IQ3_S, q4mi.T_Q8_0
+T_Q6_K, T_IQ4_NL, T_IQ2_S, T_Q2_0 = 14, 20, 22, 42
+TOL = 1e-3
+
+
+# device copies made by dev() stay referenced until host() has synchronized:
+# a temporary passed straight into an asynchronous launch would otherwise
+# return its memory to torch's cache before the kernel has read it
+_KEEP = []
+
+
+def dev(a):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    _KEEP.clear()
+    return t.cpu().numpy()
+
+
+def empty(shape, dtype):
+    import torch
+    return torch.empty(shape, dtype=dtype, device="cuda")
+
+
+@pytest.mark.parametrize("ty", [T_IQ4_NL, T_Q2_0, T_IQ2_S, T_Q6_K])
+@pytest.mark.parametrize("K,rows,nt", [(512, 131, 1), (2048, 300, 3), (4096, 64, 8)])
+def test_mmvq_formats_sums_and_y(gpu, oracle, ty, K, rows, nt):
+    import torch
+    rng = np.random.default_rng(ty * 1000 + K + nt)
+    w = synth.matrix(rng, ty, rows, K)
+    x = rng.standard_normal((nt, K)).astype(np.float32)
+    qs = np.stack([oracle.quant8(x[t])[0] for t in range(nt)])
+    ds = np.stack([oracle.quant8(x[t])[1] for t in range(nt)])
+    y = empty((nt, rows), torch.float32)
+    s = empty((nt, rows, K // 32), torch.int32)
+    q4mi.check(gpu.q4mi_mmvq(ty, q4mi.ptr(dev(w)), rows, K, q4mi.ptr(dev(qs)), q4mi.ptr(dev(ds)),
+                             nt, q4mi.ptr(y), 1.0, q4mi.ptr(s)), "q4mi_mmvq")
+    sg = host(s)
+    rb = om.row_bytes(ty, K)
+    for t in range(nt):
+        for r in range(0, rows, 5):
+            assert np.array_equal(sg[t, r], oracle.group_sums(ty, w[r * rb:(r + 1) * rb], K,
+                                                              qs[t])), (t, r)
+    assert rel_err(host(y), oracle.dot8_rows(ty, w, rows, K, x)) <= TOL
+
+
+@pytest.mark.parametrize("n", [1, 4])
+def test_q6k_lm_head(gpu, oracle, n):
+    """A Q6_K LM head (the reference's wgv_q6_k_k case) through q4_mmvq_n:
+    40000 x 2048, fp32 x quantized by the library."""
+    import torch
+    rows, K = 40000, 2048
+    rng = np.random.default_rng(600 + n)
+    w = synth.matrix(rng, T_Q6_K, rows, K)
+    x = rng.standard_normal((n, K)).astype(np.float32)
+    y = empty((n, rows), torch.float32)
+    gpu.q4_mmvq_warm()
+    q4mi.check(gpu.q4_mmvq_n(T_Q6_K, q4mi.ptr(dev(w)), rows, K, q4mi.ptr(dev(x)), q4mi.ptr(y),
+                             1.0, n), "q4_mmvq_n")
+    assert rel_err(host(y), oracle.dot8_rows(T_Q6_K, w, rows, K, x)) <= TOL
+
+
+def packed_experts(rng, E, H, F, tg, td):
+    g = synth.matrix(rng, tg, E * F, H)
+    u = synth.matrix(rng, tg, E * F, H)
+    d = synth.matrix(rng, td, E * H, F)
+    gs, ds = F * om.row_bytes(tg, H), H * om.row_bytes(td, F)
+    arena = np.concatenate([np.concatenate([g[e * gs:(e + 1) * gs], u[e * gs:(e + 1) * gs],
+                                            d[e * ds:(e + 1) * ds]]) for e in range(E)])
+    return arena, 2 * gs + ds, 0, gs, 2 * gs
+
+
+@pytest.mark.parametrize("tg,td", [(T_IQ3_S, T_IQ4_NL), (T_IQ3_S, T_Q2_0), (T_IQ2_S, T_IQ4_NL),
+                                   (T_IQ2_S, T_Q2_0), (T_IQ2_S, T_IQ2_S), (T_Q8_0, T_IQ2_S)])
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_moe_layer_formats(gpu, oracle, tg, td, n_tok):
+    """Decode (1 token, host list) and the 4-token verify window over
+    layers mixing the reference models' formats: IQ2_S / IQ3_S / Q8_0
+    gate/up with IQ4_NL / Q2_0 / IQ2_S down (hidden 2048, n_ff 512)."""
+    H, F, E = 2048, 512, 24
+    rng = np.random.default_rng(tg * 100 + td + n_tok)
+    arena, stride, og, ou, od = packed_experts(rng, E, H, F, tg, td)
+    d_arena = dev(arena)
+    x = rng.standard_normal((n_tok, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, 9, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, 9)).astype(np.float32)
+    yo = oracle.moe_tokens(H, F, tg, td, arena, stride, x, ids, w)
+    P = q4mi.ptr
+    if n_tok == 1:
+        y = dev(np.zeros(H, np.float32))
+        i0, w0 = np.ascontiguousarray(ids[0]), np.ascontiguousarray(w[0])
+        q4mi.check(gpu.q4_hip_moe_exec(P(d_arena), stride, i0.ctypes.data_as(ctypes.c_void_p),
+                                       w0.ctypes.data_as(ctypes.c_void_p), 9, tg, og, tg, ou, td,
+                                       od, P(dev(x[0])), None, None, None, P(y), F, H, H),
+                   "q4_hip_moe_exec")
+        assert rel_err(host(y), yo[0]) <= TOL
+        return
+    es = np.full((n_tok, 64), -1, np.int32)
+    ew = np.zeros((n_tok, 64), np.float32)
+    es[:, :9], ew[:, :9] = ids, w
+    assert gpu.q4_hip_moe_win_ok(tg, tg, td, H, F, n_tok)
+    y = dev(np.zeros((n_tok, H), np.float32))
+    q4mi.check(gpu.q4_hip_moe_exec_win(P(d_arena), stride, P(dev(es)), P(dev(ew)),
+                                       P(dev(np.full(n_tok, 9, np.int32))), n_tok, tg, og, tg, ou,
+                                       td, od, P(dev(x)), None, P(y), F, H, H), "exec_win")
+    assert rel_err(host(y), yo) <= TOL
+
+
+def test_format_coverage_rules(gpu):
+    """IQ4_NL and Q2_0 are down-projection types here (gate/up rejected);
+    Q6_K is an LM-head type (not in the routed layer)."""
+    assert gpu.q4_hip_moe_win_ok(T_IQ2_S, T_IQ2_S, T_Q2_0, 2048, 512, 4)
+    assert not gpu.q4_hip_moe_win_ok(T_IQ4_NL, T_IQ4_NL, T_IQ3_S, 2048, 512, 4)
+    assert not gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, T_Q6_K, 2048, 512, 4)

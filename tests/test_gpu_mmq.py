@@ -15,14 +15,23 @@ T_IQ3_S, T_Q8_0 = q4mi.T_IQ3_S, q4mi.T_Q8_0
 TOL = 1e-3
 
 
+# device copies made by dev() stay referenced until host() has synchronized:
+# a temporary passed straight into an asynchronous launch would otherwise
+# return its memory to torch's cache before the kernel has read it
+_KEEP = []
+
+
 def dev(a):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
 
 
 def host(t):
     import torch
     torch.cuda.synchronize()
+    _KEEP.clear()
     return t.cpu().numpy()
 
 

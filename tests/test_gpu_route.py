@@ -11,14 +11,23 @@ from q4mi import synth
 pytestmark = pytest.mark.gpu
 
 
+# device copies made by dev() stay referenced until host() has synchronized:
+# a temporary passed straight into an asynchronous launch would otherwise
+# return its memory to torch's cache before the kernel has read it
+_KEEP = []
+
+
 def dev(a):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
 
 
 def host(t):
     import torch
     torch.cuda.synchronize()
+    _KEEP.clear()
     return t.cpu().numpy()
 
 
