@@ -301,6 +301,31 @@ bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type,
                             const void *xq, uint64_t xrows, const int32_t *act_row,
                             const int32_t *bounds, uint64_t total_rows, void *hq,
                             const void *wx_gate, const void *wx_up);
+/* XG prefill: the same routed-expert GEMMs with fp16 activations on the
+ * MFMA tiles (weights dequantized to fp16 times 256, fp32 accumulation over
+ * the whole K).  Replaces q4_xg_on / _gu_type / _dn_type / _shape_ok /
+ * _tile_cap / _tiles / _cvt / _gu / _dn (src/q4.h:1177-1199,
+ * src/q4_xg.cu:514-616), same arguments: tiles {first routed row, rows <=
+ * 128, slot, expert}, weights at abase + slot*astride + og/ou/od, x16 / h16
+ * fp16 rows, q4_xg_gu writes h = silu(gate.x)*(up.x) as fp16 [rows][n_ff],
+ * q4_xg_dn writes fp32 [rows][n_embd] for the expert reduce.  Types here:
+ * IQ3_S and Q8_0 for both (the reference's gate/up IQ2_S / IQ3_XXS / IQ3_S /
+ * IQ4_XS, down IQ4_NL / Q2_0).  Numerics are the reference XG's, not the q8
+ * path's: this is its A/B. */
+int q4_xg_on(void);
+bool q4_xg_gu_type(uint32_t type);
+bool q4_xg_dn_type(uint32_t type);
+bool q4_xg_shape_ok(uint32_t n_embd, uint32_t n_ff);
+uint32_t q4_xg_tile_cap(uint32_t rows, uint32_t n_exp);
+uint32_t q4_xg_tiles(const uint32_t *ek, const uint32_t *ebase, const int32_t *slot,
+                     uint32_t n_exp, int32_t *out, uint32_t cap);
+bool q4_xg_cvt(const float *x, void *x16, uint64_t n);
+bool q4_xg_gu(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t og, uint64_t ou,
+              uint32_t n_embd, uint32_t n_ff, const int32_t *d_tiles, uint32_t n_tiles,
+              const void *x16, const int32_t *d_atok, void *h16);
+bool q4_xg_dn(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t od,
+              uint32_t n_ff, uint32_t n_embd, const int32_t *d_tiles, uint32_t n_tiles,
+              const void *h16, float *out);
 /* q4_hip_expert_reduce plus one extra row per token:
  * d_y[t] += sum_k rw*pd[rsrc] + xw[t]*pd[x_row0 + t] (d_xw NULL: weight 1;
  * the reference applies the shared expert's sigmoid gate there,

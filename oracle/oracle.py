@@ -61,6 +61,16 @@ class Oracle:
                                    _f32p, ctypes.c_uint32, _f32p]
         L.or_dot8q_rows.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                     _i8p, _f32p, ctypes.c_uint32, _f32p]
+        L.or_xg_tokens.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
+                                   ctypes.c_uint32, _i32p, _f32p, ctypes.c_uint32, _f32p]
+        L.or_f16_bits.restype = ctypes.c_uint16
+        L.or_f16_bits.argtypes = [ctypes.c_float]
+        L.or_xg_dequant_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p]
+        L.or_xg_gu_row.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                                   _f32p, _f32p]
+        L.or_xg_dn_row.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                                   _f32p, _f32p]
         L.or_router.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_uint32, _f32p,
                                 ctypes.c_uint32, _f32p, _f32p, _f32p]
         L.or_softmax_topk.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _f32p]
@@ -154,6 +164,41 @@ class Oracle:
                        _p(rsrc, _i32p), _p(rw, _f32p), _p(ek, _u32p), _p(stg, _i32p),
                        _p(stgn, _u32p), _p(bounds, _i32p))
         return dict(a_tok=a_tok, rsrc=rsrc, rw=rw, ek=ek, stg=stg, stgn=stgn, bounds=bounds)
+
+    def xg_dequant_row(self, ty, w, n):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        y = np.empty(n, np.float32)
+        self.L.or_xg_dequant_row(ty, _p(w, _u8p), n, _p(y, _f32p))
+        return y
+
+    def xg_gu_row(self, n_embd, n_ff, t_gu, expert, x):
+        """h = silu(g) * u of one token and expert, before the fp16 rounding."""
+        expert = np.ascontiguousarray(expert, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        h = np.empty(n_ff, np.float32)
+        assert self.L.or_xg_gu_row(n_embd, n_ff, t_gu, _p(expert, _u8p), _p(x, _f32p),
+                                   _p(h, _f32p))
+        return h
+
+    def xg_dn_row(self, n_ff, n_embd, t_d, down, h16):
+        down = np.ascontiguousarray(down, dtype=np.uint8)
+        h16 = np.ascontiguousarray(h16, dtype=np.float32)
+        pd = np.empty(n_embd, np.float32)
+        assert self.L.or_xg_dn_row(n_ff, n_embd, t_d, _p(down, _u8p), _p(h16, _f32p),
+                                   _p(pd, _f32p))
+        return pd
+
+    def xg_tokens(self, n_embd, n_ff, t_gu, t_d, arena, stride, x, ids, wts):
+        """The XG (fp16-activation) prefill layer, y [T, n_embd] from zero."""
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        ids = np.ascontiguousarray(np.atleast_2d(ids), dtype=np.int32)
+        wts = np.ascontiguousarray(np.atleast_2d(wts), dtype=np.float32)
+        T, k = ids.shape
+        y = np.zeros((T, n_embd), np.float32)
+        assert self.L.or_xg_tokens(n_embd, n_ff, t_gu, t_d, _p(arena, _u8p), stride,
+                                   _p(x, _f32p), T, _p(ids, _i32p), _p(wts, _f32p), k,
+                                   _p(y, _f32p))
+        return y
 
     def moe_tokens(self, n_embd, n_ff, t_gu, t_d, arena, stride, x, ids, wts, mode=0,
                    y_init=None, want_h=False):

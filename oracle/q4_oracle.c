@@ -597,3 +597,142 @@ int or_moe_tokens(uint32_t n_embd, uint32_t n_ff, uint32_t t_gu, uint32_t t_d,
     free(acc);
     return 1;
 }
+
+/* fp32 -> fp16 bits, round to nearest even (overflow to inf). */
+static uint16_t or_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int32_t e = (int32_t)((x >> 23) & 0xff) - 127 + 15;
+    uint32_t m = x & 0x7fffffu;
+    if (((x >> 23) & 0xff) == 0xff) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u : 0));
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {                       /* subnormal or zero */
+        if (e < -10) return (uint16_t)sign;
+        m |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t r = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (r & 1))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((uint32_t)e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1))) r++;
+    return (uint16_t)(sign | r);
+}
+static float or_fp16_round(float f) { return or_f16_to_f32(or_f32_to_f16(f)); }
+uint16_t or_f16_bits(float f) { return or_f32_to_f16(f); }
+void or_xg_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *o);
+
+/* One row of an XG (fp16) weight matrix: element = fp16(int_w * ws) with
+ * ws = fp16(block scale * 256) (IQ3_S: d * (2s+1); Q8_0: d), the reference
+ * XG's dequantization (src/q4_xg.cu:29-35, :60-80). */
+static void or_xg_row(uint32_t type, const uint8_t *w, uint64_t n, float *o) {
+    int32_t wi[32], mult;
+    for (uint64_t g = 0; g < n / 32; g++) {
+        or_group_ints(type, w, g, wi, &mult);
+        uint16_t dh;
+        memcpy(&dh, type == OR_T_Q8_0 ? w + 34 * g : w + 110 * (g / 8), 2);
+        const float ws = or_fp16_round(or_f16_to_f32(dh) * (float)mult * 256.f);
+        for (int i = 0; i < 32; i++) o[32 * g + i] = or_fp16_round((float)wi[i] * ws);
+    }
+}
+
+void or_xg_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *o) {
+    or_xg_row(type, w, n, o);
+}
+
+/* The XG prefill layer (q4_xg_gu + q4_xg_dn + the reduce): x16 = fp16(x);
+ * g, u = (W16 . x16) / 256 (exact products, sums in double, rounded to
+ * fp32); h16 = fp16(silu(g) * u); pd = (Wd16 . h16) / 256; y[t] += sum_j
+ * wts * pd in pick order (mode 1 of or_moe_tokens).  The GPU sums the same
+ * products in fp32 in MFMA order: outputs agree to fp32 accumulation error,
+ * except where that moves h across an fp16 rounding boundary. */
+int or_xg_tokens(uint32_t n_embd, uint32_t n_ff, uint32_t t_gu, uint32_t t_d,
+                 const uint8_t *base, uint64_t stride, const float *x, uint32_t T,
+                 const int32_t *ids, const float *wts, uint32_t k, float *y) {
+    const uint64_t rg = or_row_bytes(t_gu, n_embd), rd = or_row_bytes(t_d, n_ff);
+    if (!rg || !rd) return 0;
+    float *x16 = (float *)malloc(n_embd * sizeof(float));
+    float *wr = (float *)malloc((n_embd > n_ff ? n_embd : n_ff) * sizeof(float));
+    float *wr2 = (float *)malloc(n_embd * sizeof(float));
+    float *h16 = (float *)malloc(n_ff * sizeof(float));
+    float *acc = (float *)malloc(n_embd * sizeof(float));
+    for (uint32_t t = 0; t < T; t++) {
+        for (uint32_t i = 0; i < n_embd; i++) x16[i] = or_fp16_round(x[(uint64_t)t * n_embd + i]);
+        memset(acc, 0, n_embd * sizeof(float));
+        for (uint32_t j = 0; j < k; j++) {
+            const int32_t e = ids[t * k + j];
+            if (e < 0) continue;
+            const uint8_t *pe = base + (uint64_t)e * stride;
+            for (uint32_t r = 0; r < n_ff; r++) {
+                or_xg_row(t_gu, pe + r * rg, n_embd, wr);
+                or_xg_row(t_gu, pe + (uint64_t)n_ff * rg + r * rg, n_embd, wr2);
+                double sg = 0, su = 0;
+                for (uint32_t i = 0; i < n_embd; i++) {
+                    sg += (double)wr[i] * x16[i];
+                    su += (double)wr2[i] * x16[i];
+                }
+                const float g = (float)(sg / 256.0), u = (float)(su / 256.0);
+                h16[r] = or_fp16_round(g * u / (1.f + expf(-g)));
+            }
+            for (uint32_t r = 0; r < n_embd; r++) {
+                or_xg_row(t_d, pe + 2ull * n_ff * rg + r * rd, n_ff, wr);
+                double s = 0;
+                for (uint32_t i = 0; i < n_ff; i++) s += (double)wr[i] * h16[i];
+                acc[r] += wts[t * k + j] * (float)(s / 256.0);
+            }
+        }
+        for (uint32_t r = 0; r < n_embd; r++) y[(uint64_t)t * n_embd + r] += acc[r];
+    }
+    free(x16);
+    free(wr);
+    free(wr2);
+    free(h16);
+    free(acc);
+    return 1;
+}
+
+/* The two halves of or_xg_tokens for one expert, to check each GPU launch on
+ * its own: h[r] = silu(g) * u before its fp16 rounding (x rounded to fp16
+ * first), and pd[r] = (Wd16 . h16) / 256 for given fp16-valued h16. */
+int or_xg_gu_row(uint32_t n_embd, uint32_t n_ff, uint32_t t_gu, const uint8_t *pe,
+                 const float *x, float *h) {
+    const uint64_t rg = or_row_bytes(t_gu, n_embd);
+    if (!rg) return 0;
+    float *x16 = (float *)malloc(n_embd * sizeof(float));
+    float *wr = (float *)malloc(n_embd * sizeof(float));
+    float *wr2 = (float *)malloc(n_embd * sizeof(float));
+    for (uint32_t i = 0; i < n_embd; i++) x16[i] = or_fp16_round(x[i]);
+    for (uint32_t r = 0; r < n_ff; r++) {
+        or_xg_row(t_gu, pe + r * rg, n_embd, wr);
+        or_xg_row(t_gu, pe + (uint64_t)n_ff * rg + r * rg, n_embd, wr2);
+        double sg = 0, su = 0;
+        for (uint32_t i = 0; i < n_embd; i++) {
+            sg += (double)wr[i] * x16[i];
+            su += (double)wr2[i] * x16[i];
+        }
+        const float g = (float)(sg / 256.0), u = (float)(su / 256.0);
+        h[r] = g * u / (1.f + expf(-g));
+    }
+    free(x16);
+    free(wr);
+    free(wr2);
+    return 1;
+}
+
+int or_xg_dn_row(uint32_t n_ff, uint32_t n_embd, uint32_t t_d, const uint8_t *pd_w,
+                 const float *h16, float *pd) {
+    const uint64_t rd = or_row_bytes(t_d, n_ff);
+    if (!rd) return 0;
+    float *wr = (float *)malloc(n_ff * sizeof(float));
+    for (uint32_t r = 0; r < n_embd; r++) {
+        or_xg_row(t_d, pd_w + r * rd, n_ff, wr);
+        double s = 0;
+        for (uint32_t i = 0; i < n_ff; i++) s += (double)wr[i] * h16[i];
+        pd[r] = (float)(s / 256.0);
+    }
+    free(wr);
+    return 1;
+}

@@ -206,7 +206,13 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
 // Lane's A operands of group j for one weight row: A0 = values 8kh..8kh+7,
 // A1 = values 16+8kh..16+8kh+7 (IQ3_S entries 2kh, 2kh+1 / 4+2kh, 5+2kh).
-template <uint32_t TY>
+// XG mode (fp16 activations, the reference's q4_xg): the operand is the
+// dequantized weight times kXgWs in fp16 -- the exact integer times the
+// block scale kXgWs * d_w (* (2s+1)) rounded to fp16 -- and the MFMA
+// accumulates the whole K; the epilogue divides kXgWs out.
+constexpr float kXgWs = 256.f;
+
+template <uint32_t TY, bool XG = false>
 __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t j,
                                 uint32_t kh, half8_t &A0, half8_t &A1) {
     if (TY == Q4MI_T_IQ3_S) {
@@ -216,7 +222,8 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
         const uint32_t sa = R[74 + 4 * j + kh];                    // sign nibbles 2kh, 2kh+1
         const uint32_t sb = R[74 + 4 * j + 2 + kh];                // 4+2kh, 5+2kh
         const uint32_t sc = R[106 + (j >> 1)];
-        const float m = (float)(2u * ((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1u);
+        float m = (float)(2u * ((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1u);
+        if constexpr (XG) m = q4mi_h2f(lds_u16(R)) * m * kXgWs;
         const half2_t mm = {(_Float16)m, (_Float16)m};
         uint32_t o[8];
 #pragma unroll
@@ -244,12 +251,18 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
             v[q] = lds_u16(qs + off) | (lds_u16(qs + off + 2) << 16);
         }
         uint32_t o[8];
+        // XG: the block's fp16 d times kXgWs, then the product rounded to fp16
+        const _Float16 ws = XG ? (_Float16)(q4mi_h2f(lds_u16(R + 34 * j)) * kXgWs) : (_Float16)1;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
 #pragma unroll
             for (int b = 0; b < 2; b++) {
-                const _Float16 lo = (_Float16)(float)(int8_t)(v[q] >> (16 * b));
-                const _Float16 hi = (_Float16)(float)(int8_t)(v[q] >> (16 * b + 8));
+                _Float16 lo = (_Float16)(float)(int8_t)(v[q] >> (16 * b));
+                _Float16 hi = (_Float16)(float)(int8_t)(v[q] >> (16 * b + 8));
+                if constexpr (XG) {
+                    lo = lo * ws;
+                    hi = hi * ws;
+                }
                 o[2 * q + b] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
                                ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
             }
@@ -290,7 +303,7 @@ __device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barri
 __device__ inline void mmq_bar_rd() { asm volatile("s_barrier" ::: "memory"); }
 
 // One (expert, weight block, token tile) of NSUB 32-row token sub-tiles.
-template <uint32_t TY, bool FUSED, int NSUB>
+template <uint32_t TY, bool FUSED, int NSUB, bool XG = false>
 __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, uint8_t *smem,
                                                                const int4 tinfo) {
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
@@ -300,7 +313,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     // dword copies per superblock: IQ3_S two rows per copy, else linear
     constexpr uint32_t RAW_OPS = kIq ? MMQ_NB / 2 : (MMQ_NB * SSD + 63) / 64;
     constexpr uint32_t RAW_PER_WAVE = (RAW_OPS + 3) / 4;
-    constexpr uint32_t ST_OPS = NSUB + 1;                     // copies per stage per wave
+    // copies per stage per wave: the activation rows and (q8 mode) their scales
+    constexpr uint32_t ST_OPS = NSUB + (XG ? 0 : 1);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t e = (uint32_t)tinfo.x;
@@ -377,8 +391,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         const int64_t xr = a.act_row ? a.act_row[p] : p;
         arow_src[m] = a.xq + (uint64_t)xr * a.K;
     }
-    const float *drow_src;
-    {
+    const float *drow_src = nullptr;
+    if constexpr (!XG) {
         const uint32_t r = 32 * wv + lane / 2;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
         const int64_t xr = a.act_row ? a.act_row[p] : p;
@@ -398,8 +412,10 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             const _Float16 *src = arow_src[m] + s * 64 + c * 8;
             mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
         }
-        const float *dsrc = drow_src + s * 2 + (lane & 1u);
-        mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
+        if constexpr (!XG) {
+            const float *dsrc = drow_src + s * 2 + (lane & 1u);
+            mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
+        }
     };
     f32x16_t acc[NSUB], inner[NSUB];
 #pragma unroll
@@ -442,7 +458,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         auto decode = [&]() __attribute__((always_inline)) {
             const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
 #pragma unroll
-            for (int gl = 0; gl < 2; gl++) decode_a<TY>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
+            for (int gl = 0; gl < 2; gl++)
+                decode_a<TY, XG>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
         };
         if (s != 0) decode();
         // every wave is done with stage s-1 (and at a superblock start with
@@ -490,6 +507,20 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
                 }
             }
         };
+        if constexpr (XG) {
+            // the MFMA accumulates across K straight into acc
+#pragma unroll
+            for (int n = 0; n < 2 * NSUB; n++) {
+                const int gl = n / NSUB, t = n % NSUB;
+                const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;
+                const uint32_t tok = 32 * t + (lane & 31u);
+                const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
+                const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, acc[t], 0, 0, 0);
+            }
+            continue;
+        }
         float dcur;
         f32x16_t cur = prod(0, dcur);
 #pragma unroll
@@ -513,6 +544,12 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
                 }
             }
         }
+    }
+    if constexpr (XG) {
+#pragma unroll
+        for (int t = 0; t < NSUB; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][i] *= 1.f / kXgWs;   // exact (power of 2)
     }
     if (!FUSED) {
         // lane: token column 32t + lane%32, weight rows 32wv + 8b + 4kh + 0..3
@@ -567,6 +604,20 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             h[i] = g * u * __builtin_amdgcn_rcpf(1.f + __expf(-g));
             amax = fmaxf(amax, fabsf(h[i]));
         }
+        if constexpr (XG) {   // h as fp16 rows [rows][n_ff] (the XG down's input)
+            if (p < mrows) {
+                const uint64_t prow = (uint64_t)(rbase + (int32_t)p);
+                _Float16 *o = a.hq + prow * a.n_ff + nblk + col + 4 * kh;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    half4_t v;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) v[c] = (_Float16)h[4 * b + c];
+                    *(half4_t *)(o + 8 * b) = v;
+                }
+            }
+            continue;
+        }
         // the q8 group = h columns col + 0..31 of token p: this lane has
         // columns 8b + 4kh + 0..3, the partner lane (lane ^ 32) the rest
         amax = fmaxf(amax, __shfl_xor(amax, 32));
@@ -597,7 +648,7 @@ __global__ __launch_bounds__(256) void swiglu_k(const float *__restrict__ gu,
     h[i] = g / (1.f + expf(-g)) * u;
 }
 
-template <uint32_t TY, bool FUSED>
+template <uint32_t TY, bool FUSED, bool XG = false>
 __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t ti = blockIdx.y;
@@ -606,10 +657,10 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     const int32_t rows = tinfo.z;
     // block-uniform choice of the (branch-free) sub-tile count
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
-    case 4: mmq_tile<TY, FUSED, 4>(a, smem, tinfo); break;
-    case 3: mmq_tile<TY, FUSED, 3>(a, smem, tinfo); break;
-    case 2: mmq_tile<TY, FUSED, 2>(a, smem, tinfo); break;
-    default: mmq_tile<TY, FUSED, 1>(a, smem, tinfo); break;
+    case 4: mmq_tile<TY, FUSED, 4, XG>(a, smem, tinfo); break;
+    case 3: mmq_tile<TY, FUSED, 3, XG>(a, smem, tinfo); break;
+    case 2: mmq_tile<TY, FUSED, 2, XG>(a, smem, tinfo); break;
+    default: mmq_tile<TY, FUSED, 1, XG>(a, smem, tinfo); break;
     }
 }
 
@@ -647,11 +698,11 @@ bool mmq_quant(const float *x, const int32_t *ids, void *xq, uint64_t cols, uint
     return launch_ok("mmq_quant_k");
 }
 
-template <uint32_t TY, bool FUSED>
+template <uint32_t TY, bool FUSED, bool XG = false>
 static bool set_lds_attr() {
     static bool done = false;
     if (done) return true;
-    if (hipFuncSetAttribute((const void *)mmq_k<TY, FUSED>,
+    if (hipFuncSetAttribute((const void *)mmq_k<TY, FUSED, XG>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)sizeof(MmqLds<TY>)) != hipSuccess) {
         set_error("mmq: cannot raise the LDS limit to %zu bytes", sizeof(MmqLds<TY>));
@@ -666,6 +717,31 @@ static bool mmq_launch(const MmqArgs &a, dim3 grid) {
     if (!set_lds_attr<TY, FUSED>()) return false;
     mmq_k<TY, FUSED><<<grid, dim3(256), sizeof(MmqLds<TY>), stream()>>>(a);
     return launch_ok("mmq_k");
+}
+
+template <uint32_t TY, bool FUSED>
+static bool xg_launch(const MmqArgs &a, dim3 grid) {
+    if (!set_lds_attr<TY, FUSED, true>()) return false;
+    mmq_k<TY, FUSED, true><<<grid, dim3(256), sizeof(MmqLds<TY>), stream()>>>(a);
+    return launch_ok("mmq_k (xg)");
+}
+
+// The reference's XG tile table {first routed row, rows (<= 128), slot,
+// expert} -> this kernel's tile entries (slot as the weight index, first
+// row, rows) and the tile count, on the stream (graph-capturable).
+__global__ void xg_tiles_k(const int32_t *__restrict__ in, uint32_t n, int4 *__restrict__ out,
+                           uint32_t *__restrict__ count) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = make_int4(in[4 * i + 2], in[4 * i], in[4 * i + 1], 0);
+    if (i == 0) *count = n;
+}
+
+__global__ void xg_cvt_k(const float4 *__restrict__ x, half4_t *__restrict__ y, uint64_t n4) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n4) {
+        const float4 v = x[i];
+        y[i] = half4_t{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    }
 }
 
 // xq holds xrows activation rows; act_row (optional) maps packed row p to
@@ -927,6 +1003,129 @@ bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type,
                    n_expert + (wx_gate ? 1u : 0u), xq, xrows, act_row, bounds, total_rows,
                    nullptr, 0, hq, (const uint8_t *)wx_gate, (const uint8_t *)w_up,
                    (const uint8_t *)wx_up);
+}
+
+/* ---------------------------------------------------------- XG prefill
+ * fp16-activation prefill GEMMs on the same MFMA tiles (the reference's
+ * q4_xg, src/q4_xg.cu, src/q4.h:1177-1199): weights dequantized to fp16
+ * (times 256), activations fp16, fp32 accumulation over the whole K; gate/up
+ * writes h = silu(g)*u as fp16 rows, down writes fp32 rows.  Here gate/up
+ * IQ3_S or Q8_0 and down IQ3_S or Q8_0 (the reference: gate/up IQ2_S /
+ * IQ3_XXS / IQ3_S / IQ4_XS, down IQ4_NL / Q2_0). */
+int q4_xg_on(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4_XG");
+        v = !(e && e[0] == '0');
+    }
+    return v;
+}
+bool q4_xg_gu_type(uint32_t t) { return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0; }
+bool q4_xg_dn_type(uint32_t t) { return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0; }
+bool q4_xg_shape_ok(uint32_t n_embd, uint32_t n_ff) {
+    return n_embd % MMQ_NB == 0 && n_ff % 64 == 0 && n_embd % 512 == 0 && n_ff % 512 == 0 &&
+           n_embd <= 65536 && n_ff <= 65536;
+}
+uint32_t q4_xg_tile_cap(uint32_t rows, uint32_t n_exp) { return rows / MMQ_MB + n_exp; }
+
+/* Host tile table: tiles of <= 128 routed rows per expert,
+ * out[4i..] = {first row, rows, slot, expert}; 0 when cap is too small. */
+uint32_t q4_xg_tiles(const uint32_t *ek, const uint32_t *ebase, const int32_t *slot,
+                     uint32_t n_exp, int32_t *out, uint32_t cap) {
+    uint32_t n = 0;
+    for (uint32_t e = 0; e < n_exp; e++)
+        for (uint32_t t = 0; t < ek[e]; t += MMQ_MB) {
+            if (n >= cap) return 0;
+            out[4 * n + 0] = (int32_t)(ebase[e] + t);
+            out[4 * n + 1] = (int32_t)(ek[e] - t < (uint32_t)MMQ_MB ? ek[e] - t : MMQ_MB);
+            out[4 * n + 2] = slot[e];
+            out[4 * n + 3] = (int32_t)e;
+            n++;
+        }
+    return n;
+}
+
+/* x16[i] = fp16(x[i]), n % 4 == 0. */
+bool q4_xg_cvt(const float *x, void *x16, uint64_t n) {
+    if (!n) return true;
+    if (!x || !x16 || n % 4 || ((uintptr_t)x & 15) || ((uintptr_t)x16 & 7)) {
+        set_error("q4_xg_cvt: bad arguments");
+        return false;
+    }
+    const uint64_t n4 = n / 4;
+    xg_cvt_k<<<dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, stream()>>>(
+        (const float4 *)x, (half4_t *)x16, n4);
+    return launch_ok("xg_cvt_k");
+}
+
+static bool xg_args(uint32_t type, const uint8_t *w, uint64_t astride, uint32_t K,
+                    const int32_t *d_tiles, uint32_t n_tiles, MmqArgs &a, const char *who) {
+    if (!w || !d_tiles || (((uintptr_t)w) & 3u) || (astride & 3u)) {
+        set_error("%s: bad arguments", who);
+        return false;
+    }
+    if (!ensure_tiles(n_tiles)) {
+        set_error("%s: tile buffer allocation failed", who);
+        return false;
+    }
+    xg_tiles_k<<<dim3((n_tiles + 255) / 256), dim3(256), 0, stream()>>>(d_tiles, n_tiles,
+                                                                       g_tiles, g_ntiles);
+    if (!launch_ok("xg_tiles_k")) return false;
+    a = MmqArgs{};
+    a.w = w;
+    a.estride = astride;
+    a.rb = (uint32_t)q4mi_row_bytes(type, K);
+    a.K = K;
+    a.tiles = g_tiles;
+    a.ntiles = g_ntiles;
+    a.mt = MMQ_MB;
+    return true;
+}
+
+/* h16[row][n_ff] = fp16(silu(gate . x16[atok[row]]) * (up . x16[atok[row]]))
+ * over the tiles; expert weights at abase + slot*astride + og / ou. */
+bool q4_xg_gu(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t og, uint64_t ou,
+              uint32_t n_embd, uint32_t n_ff, const int32_t *d_tiles, uint32_t n_tiles,
+              const void *x16, const int32_t *d_atok, void *h16) {
+    if (!n_tiles) return true;
+    if (!q4_xg_gu_type(type) || !q4_xg_shape_ok(n_embd, n_ff) || !x16 || !h16 ||
+        ((uintptr_t)x16 & 15) || ((og ^ ou) & 3u)) {
+        set_error("q4_xg_gu: type/shape not covered");
+        return false;
+    }
+    MmqArgs a;
+    if (!abase || !xg_args(type, abase + og, astride, n_embd, d_tiles, n_tiles, a, "q4_xg_gu"))
+        return false;
+    a.up_off = ou - og;
+    a.n_ff = n_ff;
+    a.xq = (const _Float16 *)x16;
+    a.act_row = d_atok;
+    a.hq = (_Float16 *)h16;
+    const dim3 grid(n_ff / 64, n_tiles);
+    return type == Q4MI_T_IQ3_S ? xg_launch<Q4MI_T_IQ3_S, true>(a, grid)
+                                : xg_launch<Q4MI_T_Q8_0, true>(a, grid);
+}
+
+/* out[row][n_embd] (fp32) = down . h16[row] over the tiles; expert down
+ * matrices at abase + slot*astride + od. */
+bool q4_xg_dn(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t od,
+              uint32_t n_ff, uint32_t n_embd, const int32_t *d_tiles, uint32_t n_tiles,
+              const void *h16, float *out) {
+    if (!n_tiles) return true;
+    if (!q4_xg_dn_type(type) || !q4_xg_shape_ok(n_embd, n_ff) || !h16 || !out ||
+        ((uintptr_t)h16 & 15) || ((uintptr_t)out & 15)) {
+        set_error("q4_xg_dn: type/shape not covered");
+        return false;
+    }
+    MmqArgs a;
+    if (!abase || !xg_args(type, abase + od, astride, n_ff, d_tiles, n_tiles, a, "q4_xg_dn"))
+        return false;
+    a.xq = (const _Float16 *)h16;
+    a.dst = out;
+    a.ld = n_embd;
+    const dim3 grid(n_embd / MMQ_NB, n_tiles);
+    return type == Q4MI_T_IQ3_S ? xg_launch<Q4MI_T_IQ3_S, false>(a, grid)
+                                : xg_launch<Q4MI_T_Q8_0, false>(a, grid);
 }
 
 /* h[r][k] = silu(gu[r][k]) * gu[r][n_ff + k]. */

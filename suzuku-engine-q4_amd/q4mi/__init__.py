@@ -98,6 +98,15 @@ _SIGS = {
                                _u64]),
     "q4mi_mmq_gate_up_parts": (_b, [_vp, _vp, _u32, _u64, _u64, _u64, _u32, _vp, _u64, _vp,
                                     _vp, _u64, _vp, _vp, _vp]),
+    "q4_xg_on": (_c.c_int, []),
+    "q4_xg_gu_type": (_b, [_u32]),
+    "q4_xg_dn_type": (_b, [_u32]),
+    "q4_xg_shape_ok": (_b, [_u32, _u32]),
+    "q4_xg_tile_cap": (_u32, [_u32, _u32]),
+    "q4_xg_tiles": (_u32, [_vp, _vp, _vp, _u32, _vp, _u32]),
+    "q4_xg_cvt": (_b, [_vp, _vp, _u64]),
+    "q4_xg_gu": (_b, [_u32, _vp, _u64, _u64, _u64, _u32, _u32, _vp, _u32, _vp, _vp, _vp]),
+    "q4_xg_dn": (_b, [_u32, _vp, _u64, _u64, _u32, _u32, _vp, _u32, _vp, _vp]),
     "q4mi_expert_reduce_x": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u64, _vp]),
 }
 

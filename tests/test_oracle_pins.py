@@ -305,3 +305,28 @@ def test_sgate_closed_form(oracle):
     _, sg = oracle.router(0, w, 4, K, x, sgw=g)
     d = x.astype(np.float64) @ g.astype(np.float64)
     assert np.allclose(sg, 1 / (1 + np.exp(-d)), rtol=1e-6, atol=0)
+
+
+def test_xg_fp16_rounding(oracle):
+    """The XG oracle's fp32 -> fp16 conversion equals numpy's (IEEE round to
+    nearest even) on normals, subnormals, ties, overflow and signed zero."""
+    rng = np.random.default_rng(12)
+    v = np.concatenate([rng.standard_normal(4000) * 10 ** rng.uniform(-9, 5, 4000),
+                        np.array([0.0, -0.0, 65504.0, 65520.0, 70000.0, 6e-8, 3e-8, 1e-9,
+                                  1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -2049.0, 2051.0])
+                        ]).astype(np.float32)
+    got = np.array([oracle.L.or_f16_bits(float(f)) for f in v], np.uint16)
+    assert np.array_equal(got, v.astype(np.float16).view(np.uint16))
+
+
+def test_xg_dequant_close_to_float_dequant(oracle):
+    """XG weights (fp16 of the integer times fp16(scale * 256)) are the
+    float dequantization times 256 to two fp16 roundings."""
+    rng = np.random.default_rng(13)
+    for ty in (om.T_IQ3_S, om.T_Q8_0):
+        w = synth.matrix(rng, ty, 3, 2048)
+        rb = om.row_bytes(ty, 2048)
+        for r in range(3):
+            a = oracle.xg_dequant_row(ty, w[r * rb:(r + 1) * rb], 2048).astype(np.float64)
+            b = oracle.dequant_row(ty, w[r * rb:(r + 1) * rb], 2048).astype(np.float64) * 256
+            assert np.all(np.abs(a - b) <= 2 * 2 ** -11 * np.abs(b) + 1e-30)
