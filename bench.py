@@ -66,9 +66,8 @@ def routes(rng, L):
 def cpu_baseline(seconds=12.0):
     """The reference CPU expert job on this host (bounded sample)."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as om
     from q4mi import synth
+    om = _oracle()
     rng = np.random.default_rng(5)
     arena = synth.expert_arena(rng, N_EXP + 1, N_EMBD, N_FF)
     stride = synth.expert_stride(N_EMBD, N_FF)[0]
@@ -105,6 +104,126 @@ def cpu_baseline(seconds=12.0):
             "kind": kind,
             "sample": "%d config-2 decode layers (11 IQ3_S experts each, routes rotating over "
                       "a 693 MB arena), median %.1f us/layer" % (len(times), med * 1e6)}
+
+
+def _oracle():
+    """The checker package (oracle/: the reference's CPU path and the C
+    restatement), used only for the CPU baselines."""
+    p = os.path.join(ROOT, "oracle")
+    if p not in sys.path:
+        sys.path.insert(0, p)
+    import oracle as om
+    return om
+
+
+def host_facts():
+    """nproc, CPU model and the ISA path the reference's CPU kernels take."""
+    om = _oracle()
+    model = "?"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    isa = None
+    if om.have_ref():
+        isa = ("AVX-512 VNNI/VBMI/BITALG (c6_* kernels)" if om.Ref().L.qref_has512()
+               else "AVX2 (+FMA/F16C) kernels")
+    return {"nproc": nproc, "cpu_model": model, "isa_path": isa}
+
+
+def _timed(run, seconds, min_n=3):
+    import numpy as np
+    run(0)
+    times, i = [], 1
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_n:
+        t0 = time.perf_counter()
+        run(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    return float(np.median(times)), len(times)
+
+
+def cpu_baselines(facts, seconds=4.0):
+    """The reference's CPU path (oracle/_ref, compiled from its sources) on
+    the other BASELINE configs, each a bounded sample: configs[0] (cpx_dot8
+    IQ3_S rows, OpenMP over rows), configs[2] (q4_cpuex_dispatch_win, 4
+    tokens), configs[3] (no CPU prefill exists: q4_cpuex_dispatch_win over
+    4-token windows, a sample of the 512 windows of the 2048-token prompt)
+    and configs[4] (cpx_dot8 / cpx_dot8n Q8_0 rows, n = 1 and 4)."""
+    import numpy as np
+    from q4mi import synth
+    om = _oracle()
+    if not om.have_ref():
+        return None
+    R = om.Ref()
+    th = min(16, facts["nproc"])
+    out = {"threads_rows": th, "threads_expert_pool": int(R.L.qref_threads())}
+    rng = np.random.default_rng(8)
+    # configs[0]: 4096 x 4096 IQ3_S, copies rotated beyond the host caches
+    K = 4096
+    ws = [synth.matrix(rng, om.T_IQ3_S, K, K) for _ in range(100)]
+    x = rng.standard_normal(K).astype(np.float32)
+    med, n = _timed(lambda i: R.dot8_rows(om.T_IQ3_S, ws[i % len(ws)], K, K, x, th), seconds)
+    nb = 4096 * 4096 // 256 * 110 + 2 * 4 * K
+    out["config0_gemv"] = {"us": round(med * 1e6, 1), "GB/s": round(nb / med / 1e9, 2),
+                           "sample": "%d calls over 100 rotating 7.2 MB copies (720 MB)" % n}
+    del ws
+    # configs[2] / [3]: one layer's arena (693 MB)
+    arena = synth.expert_arena(rng, N_EXP + 1, N_EMBD, N_FF)
+    stride = synth.expert_stride(N_EMBD, N_FF)[0]
+
+    def win(xs, rts):
+        ids = np.concatenate([r[0] for r in rts])
+        w = np.concatenate([r[1] for r in rts])
+        tn = np.array([len(r[0]) for r in rts], np.uint32)
+        R.moe_win(N_EMBD, N_FF, om.T_IQ3_S, om.T_IQ3_S, N_EXP + 1, arena, stride, xs, ids, w, tn)
+        return len(set(ids.tolist()))
+
+    x4 = rng.standard_normal((4, N_EMBD)).astype(np.float32)
+    w4 = [routes(rng, 4) for _ in range(32)]
+    med, n = _timed(lambda i: win(x4, w4[i % 32]), seconds)
+    uq = np.mean([len(set(np.concatenate([r[0] for r in rr]).tolist())) for rr in w4])
+    nb = uq * EXPERT_BYTES + 2 * 4 * 4 * N_EMBD
+    out["config3_window"] = {"us": round(med * 1e6, 1), "GB/s": round(nb / med / 1e9, 2),
+                             "sample": "%d 4-token windows (q4_cpuex_dispatch_win)" % n}
+    # the reference's window takes at most 64 (token, expert) entries, so
+    # top-10 + shared (11 per token) fits 4 tokens, not 8
+    xw = rng.standard_normal((4, N_EMBD)).astype(np.float32)
+    lgz = synth.logits(rng, 64, N_EXP, zipf=True)
+    idz, wz = R.softmax_topk(lgz, TOPK)
+    wzs = [[(np.append(idz[4 * j + t], N_EXP).astype(np.int32),
+             np.append(wz[4 * j + t], 1.0).astype(np.float32)) for t in range(4)]
+           for j in range(16)]
+    med, n = _timed(lambda i: win(xw, wzs[i % 16]), seconds)
+    out["config3_prefill"] = {"us_per_4_token_window": round(med * 1e6, 1),
+                              "layer_us_512_windows": round(512 * med * 1e6, 1),
+                              "tok_per_s": round(4 / med, 1),
+                              "sample": "%d 4-token windows of Zipf-routed tokens (top-10 + "
+                                        "shared); the reference has no CPU prefill, so the "
+                                        "2048-token layer is 512 such windows (its window takes "
+                                        "at most 64 (token, expert) entries: 8 tokens x 11 do "
+                                        "not fit)" % n}
+    del arena
+    # configs[4]: Q8_0 151936 x 2048
+    rows = 151936
+    w3 = [synth.matrix(rng, om.T_Q8_0, rows, N_EMBD) for _ in range(3)]
+    for nt in (1, 4):
+        xs = rng.standard_normal((nt, N_EMBD)).astype(np.float32)
+        med, n = _timed(lambda i: R.dot8_rows(om.T_Q8_0, w3[i % 3], rows, N_EMBD, xs, th),
+                        seconds / 2)
+        nb = rows * 2176 + 4 * nt * N_EMBD + 4 * nt * rows
+        out["config4_lmhead_n%d" % nt] = {"us": round(med * 1e6, 1),
+                                          "GB/s": round(nb / med / 1e9, 2),
+                                          "sample": "%d calls rotating 3 copies (990 MB)" % n}
+    return out
 
 
 def main():
@@ -230,7 +349,8 @@ def main():
         "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ3_S experts generated in HBM; N(0,1) activations)",
-        "config": {"workload": "config 2: IQ3_S MoE decode layer, 1 token, hidden 2048, "
+        "config": {"workload": "BASELINE.json configs[1] (config 2): IQ3_S MoE decode layer, "
+                               "1 token, hidden 2048, "
                                "512 routed experts top-10 + 1 shared, expert intermediate 512; "
                                "sustained over a %d-layer stack of distinct experts" % NL,
                    "layers_per_step": NL, "bytes_per_layer": LAYER_BYTES},
@@ -246,6 +366,8 @@ def main():
     if not args.no_extra:
         out["config3_window"] = bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
                                              capture, timed, args)
+        out["config2_routed"] = bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
+                                             capture, timed, args)
     del g_full, g_gu, g_dn, arenas
     torch.cuda.empty_cache()
 
@@ -254,15 +376,22 @@ def main():
         out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
         out["prefill"]["pct_of_measured_int8_peak"] = round(
             100 * out["prefill"]["mmq_TOPS"] / out["mfma_peak"]["int8_TOPS"], 2)
+        out["prefill_xg"] = bench_prefill_xg(L, torch, np, q4mi, synth, args)
     if not args.no_extra:
-        out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1)
+        out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1,
+                                         "configs[0]")
         out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
-                                              2048, 2, 1)
+                                              2048, 2, 1, "configs[4]")
         out["config4_lmhead_n4"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
-                                              2048, 2, 4)
+                                              2048, 2, 4, "configs[4]")
     if not args.no_cpu:
+        facts = host_facts()
         out["cpu_baseline"] = cpu_baseline()
-    print(json.dumps(out))
+        out["cpu_baseline"].update({k: facts[k] for k in ("cpu_model", "isa_path")})
+        out["cpu_baseline"]["nproc"] = facts["nproc"]
+        out["cpu_baselines"] = cpu_baselines(facts)
+    sys.stdout.write(json.dumps(out) + "\n")
+    sys.stdout.flush()
 
 
 def bench_mfma_peak(L, torch, q4mi, iters=16384, reps=5):
@@ -363,13 +492,135 @@ def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
     used = int((ek > 0).sum().item())
     wbytes = (used + 1) * EXPERT_BYTES
     del arenas
-    return {"layer_us": round(t * 1e6, 1), "tok_per_s": round(T / t, 1),
-            "mmq_TOPS": round(PF_OPS / t / 1e12, 2),
+    return {"baseline_config": "configs[3]", "layer_us": round(t * 1e6, 1),
+            "tok_per_s": round(T / t, 1), "mmq_TOPS": round(PF_OPS / t / 1e12, 2),
             "pct_of_int8_peak": round(100 * PF_OPS / t / 5.0e15, 2),
             "experts_touched": used, "weight_bytes": wbytes,
             "weight_GB_per_s": round(wbytes / t / 1e9, 1),
             "note": "whole routed layer incl. route, pack, quantize, SwiGLU, reduce and the "
                     "shared expert; ops = (20480 + 2048) rows x 3 x 2048 x 512 x 2"}
+
+
+def bench_prefill_xg(L, torch, np, q4mi, synth, args, copies=3, reps=10):
+    """The XG A/B of the prefill layer (the reference's q4_xg: fp16
+    activations, fp16-dequantized weights, fp32 accumulation) on the same
+    routing as bench_prefill: q4_xg_cvt -> q4_xg_gu -> q4_xg_dn -> reduce, the
+    shared expert as one more tile set over every token.  The tile table is
+    built on the host from the pack (as the reference does) before timing;
+    x is N(0,1) * 0.05 so h stays in fp16's range."""
+    T, k, E, H, F = PF_T, PF_K, N_EXP, N_EMBD, N_FF
+    stride, og, ou, od = synth.expert_stride(H, F)
+    rows = T * k
+    rng = np.random.default_rng(99)
+    arenas = [synth.device_iq3s((E + 1) * stride, seed=500 + c) for c in range(copies)]
+    x = torch.randn(T, H, device="cuda") * 0.05
+    lg = torch.from_numpy(synth.logits(rng, T, E, zipf=True)).cuda()
+    i32 = torch.int32
+    P, chk, TY = q4mi.ptr, q4mi.check, q4mi.T_IQ3_S
+    ids, wts = torch.empty(T, k, dtype=i32, device="cuda"), torch.empty(T, k, device="cuda")
+    a_tok = torch.empty(rows + T, dtype=i32, device="cuda")
+    a_tok[rows:] = torch.arange(T, dtype=i32, device="cuda")
+    rsrc = torch.empty(rows, dtype=i32, device="cuda")
+    rw = torch.empty(rows, device="cuda")
+    stg, stgn = torch.empty(512, dtype=i32, device="cuda"), torch.empty(1, dtype=i32, device="cuda")
+    ek = torch.empty(512, dtype=i32, device="cuda")
+    bounds = torch.empty(E + 1, dtype=i32, device="cuda")
+    chk(L.q4_hip_route_pf(P(lg), P(ids), P(wts), T, E, k), "route")
+    chk(L.q4mi_assign(P(ids), P(wts), P(a_tok), P(rsrc), P(rw), P(stg), P(stgn), P(ek),
+                      P(bounds), T, k, E, T), "assign")
+    torch.cuda.synchronize()
+    ekh = np.append(ek.cpu().numpy()[:E], T).astype(np.uint32)
+    ebh = np.append(bounds.cpu().numpy()[:E], rows).astype(np.uint32)
+    slot = np.arange(E + 1, dtype=np.int32)
+    cap = L.q4_xg_tile_cap(rows + T, E + 1)
+    tiles = np.zeros(4 * cap, np.int32)
+    nt = L.q4_xg_tiles(ekh.ctypes.data, ebh.ctypes.data, slot.ctypes.data, E + 1,
+                       tiles.ctypes.data, cap)
+    assert nt > 0
+    d_tiles = torch.from_numpy(tiles[:4 * nt]).cuda()
+    x16 = torch.empty(T, H, dtype=torch.float16, device="cuda")
+    h16 = torch.empty(rows + T, F, dtype=torch.float16, device="cuda")
+    pd = torch.empty(rows + T, H, device="cuda")
+    y = torch.zeros(T, H, device="cuda")
+
+    def layer(c):
+        A = arenas[c].data_ptr()
+        chk(L.q4_xg_cvt(P(x), P(x16), T * H), "xg cvt")
+        chk(L.q4_xg_gu(TY, A, stride, og, ou, H, F, P(d_tiles), nt, P(x16), P(a_tok), P(h16)),
+            "xg gu")
+        chk(L.q4_xg_dn(TY, A, stride, od, F, H, P(d_tiles), nt, P(h16), P(pd)), "xg dn")
+        chk(L.q4mi_expert_reduce_x(P(y), P(pd), P(rsrc), P(rw), T, k, H, rows, None), "reduce")
+
+    def run_all():
+        for c in range(copies):
+            layer(c)
+
+    run_all()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q4mi.use_torch_stream()
+        run_all()
+    q4mi.use_torch_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    del arenas, g
+    return {"baseline_config": "configs[3] (A/B)", "layer_us": round(t * 1e6, 1),
+            "tok_per_s": round(T / t, 1), "fp16_TFLOPS": round(PF_OPS / t / 1e12, 2),
+            "pct_of_fp16_peak": round(100 * PF_OPS / t / 2.5e15, 2), "tiles": int(nt),
+            "note": "fp16 activations (XG): excludes routing/pack (the tile table is "
+                    "host-built from the pack, as in the reference); includes x->fp16, "
+                    "gate/up, down, reduce"}
+
+
+def bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, timed, args):
+    """configs[1] with its router in front (the f1/f2 row): per layer
+    q4mi_moe_route (fp32 512 x 2048 router GEMV, the shared expert's sigmoid
+    gate, softmax top-10 into the device list with the shared expert at
+    weight sg) then q4_hip_moe_exec_dev, sustained over the layer stack.
+    Bytes per layer add the 4 MB router and the 8 KB gate vector."""
+    P = q4mi.ptr
+    T = q4mi.T_IQ3_S
+    g = torch.Generator("cuda").manual_seed(11)
+    routers = torch.randn(NL, N_EXP, N_EMBD, device="cuda", generator=g) * 0.05
+    sgate = torch.randn(NL, N_EMBD, device="cuda", generator=g) * 0.02
+    xs = torch.randn(NL, N_EMBD, device="cuda", generator=g)
+    ys = torch.zeros(NL, N_EMBD, device="cuda")
+    lg = torch.empty(NL, N_EXP, device="cuda")
+    es = torch.empty(NL, 64, dtype=torch.int32, device="cuda")
+    ew = torch.empty(NL, 64, device="cuda")
+    nh = torch.empty(NL, dtype=torch.int32, device="cuda")
+    sg = torch.empty(NL, device="cuda")
+
+    def stack():
+        for l in range(NL):
+            q4mi.check(L.q4mi_moe_route(P(routers[l]), 0, P(sgate[l]), P(xs[l]), 1, N_EMBD, N_EXP,
+                                        TOPK, P(lg[l]), P(es[l]), P(ew[l]), P(nh[l]), 64, N_EXP,
+                                        P(sg[l])), "q4mi_moe_route")
+            q4mi.check(L.q4_hip_moe_exec_dev(arenas[l].data_ptr(), stride, P(es[l]), P(ew[l]),
+                                             P(nh[l]), T, og, T, ou, T, od, P(xs[l]), None, None,
+                                             None, P(ys[l]), N_FF, N_EMBD, N_EMBD),
+                       "q4_hip_moe_exec_dev")
+    gr = capture(stack)
+    steps = max(args.steps // 4, 10)
+    ms = timed(gr, steps, max(args.warmup // 4, 2))
+    t = ms * 1e-3 / (steps * NL)
+    nbytes = LAYER_BYTES + N_EXP * N_EMBD * 4 + N_EMBD * 4
+    del gr
+    return {"baseline_config": "configs[1] + router", "layer_us": round(t * 1e6, 3),
+            "GB/s": round(nbytes / t / 1e9, 1),
+            "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
+            "bytes_per_layer": nbytes,
+            "note": "router GEMV (fp32 512x2048) + sigmoid shared gate + top-10 into device "
+                    "lists, then the device-list decode layer; graph over the %d-layer stack"
+                    % NL}
 
 
 def bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, timed, args,
@@ -417,14 +668,15 @@ def bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, ti
     t = ms * 1e-3 / (steps * NL)
     nbytes = float(np.mean(uniq)) * EXPERT_BYTES + 2 * 4 * n_tok * N_EMBD
     del g
-    return {"layer_us": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+    return {"baseline_config": "configs[2]", "layer_us": round(t * 1e6, 3),
+            "GB/s": round(nbytes / t / 1e9, 1),
             "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
             "unique_experts": round(float(np.mean(uniq)), 2), "tokens": n_tok,
             "note": "4 tokens, own top-10 each + shared; each unique expert read once; "
                     "graph over the %d-layer stack" % NL}
 
 
-def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):
+def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, label, reps=30):
     """q4_mmvq_n over `copies` distinct weight copies (rotated to defeat the
     Infinity Cache); GB/s = (weights + x + y) / kernel-pair time."""
     rb = q4mi.row_bytes(ty, K)
@@ -449,7 +701,8 @@ def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, reps=30):
     t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
     nbytes = rows * rb + 4 * nt * K + 4 * nt * rows
     del ws
-    return {"us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+    return {"baseline_config": label, "us": round(t * 1e6, 2),
+            "GB/s": round(nbytes / t / 1e9, 1),
             "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
             "note": "fp32 x in, q8 quantization included (inside the GEMV blocks for <= 1024 row tiles, else one quantize launch); eager launches"}
 
