@@ -116,12 +116,17 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
     a.src = src;
     a.hl = hl;
     a.gplan = work.h ? work.plan : g_plan;
+    // a producer publishes each chunk before issuing its next one: a copy
+    // issue stalls while the memory system is saturated, and publishing only
+    // after the next chunk's issue delayed the first chunk by microseconds
+    a.ahead = 1;
     a.plan_in = (g_phases & 1) ? 1u : 0u;   // down follows this call's gate/up
 #ifdef Q4MI_TRACE
     if (!work.h && !g_trace && hipMalloc(&g_trace, 2 * 4096 * 32 * 8) == hipSuccess)
         (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
     a.trace = g_trace;
     a.dbg = getenv("Q4MI_DBG") ? (uint32_t)atoi(getenv("Q4MI_DBG")) : 0u;
+    if (getenv("Q4MI_AHEAD")) a.ahead = (uint32_t)atoi(getenv("Q4MI_AHEAD"));
 #endif
     const uint32_t nt = src.n_tok;
     if (nt == 1) return run_nt<1>(gt, dt, a, nu_host);

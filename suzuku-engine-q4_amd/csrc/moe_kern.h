@@ -390,6 +390,7 @@ struct MoeArgs {
     uint32_t n_embd;
     uint32_t rb_gu, rb_dn;
     uint32_t chunk;   // gate/up: pairs per chunk; down: experts per chunk
+    uint32_t ahead;   // chunks a producer may have issued and not yet published (<= kMaxS)
     uint32_t slots;   // LDS ring slots (<= kMaxS)
     uint32_t nsel_cap;  // down: q8(h) rows the LDS holds
     const float *x;   // [n_tok][K]
@@ -521,7 +522,7 @@ __device__ inline void wait_chunk(const Sync *y, uint32_t c) {
 // unpublished, so it cannot hold back a chunk the consumers are waiting for.
 template <class IssueFn, class ItemsFn>
 __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, uint32_t S,
-                               uint32_t &issued, IssueFn issue, ItemsFn items
+                               uint32_t ahead, uint32_t &issued, IssueFn issue, ItemsFn items
 #ifdef Q4MI_TRACE
                                , unsigned long long *q4tr = nullptr, uint32_t q4kern = 0
 #endif
@@ -543,7 +544,7 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
     uint32_t npub = 0, nloop = 0;
 #endif
     while (pub < C && idle < kSpinMax) {
-        while (next < C && (next < pub + kProd * kMaxS) && slot_free(next)) {
+        while (next < C && (next < pub + kProd * ahead) && slot_free(next)) {
             if (next >= S) lds_st(&y->cons[next % S], 0);
             lds_st(&y->owner[next % S], next);
             issue(next);
@@ -596,6 +597,30 @@ __device__ inline uint32_t share_lo(uint32_t PT, uint32_t bid, uint32_t nblk) {
     return (uint32_t)(((uint64_t)PT * bid) / nblk);
 }
 
+// First pair of block `bid` when the blocks split the pairs by work: a pair
+// of unique expert u costs 2 + (tokens that picked u) -- one decode of its
+// gate and up rows shared by all of them, one dot per token -- so the
+// blocks holding an expert every token picked (the shared expert) get fewer
+// pairs.  Every wave computes the same value (lane u: expert u).
+__device__ inline uint32_t share_weighted(const Plan *P, uint32_t nu, uint32_t n_ff,
+                                          uint32_t bid, uint32_t nblk, uint32_t lane) {
+    const uint32_t c = lane < nu ? 2u + (uint32_t)__popc(P->sel[lane]) : 0u;
+    const uint32_t incl = q4mi_wave_incl_scan(c);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    if (bid >= nblk) return nu * n_ff;
+    // target in units of 1/n_ff of an expert's cost: t = total * n_ff * bid /
+    // nblk (< 2^32: total <= 64 * 10, n_ff <= 1024, bid < 4096)
+    const uint32_t t = total * n_ff * bid / nblk;
+    // expert u0 = number of experts whose whole cost ends at or before t
+    const uint64_t done = __ballot(incl * n_ff <= t && lane < nu);
+    const uint32_t u0 = (uint32_t)__popcll(done);
+    if (u0 >= nu) return nu * n_ff;
+    const uint32_t ex = (uint32_t)__builtin_amdgcn_readlane((int)(incl - c), (int)u0);
+    const uint32_t cu = (uint32_t)__builtin_amdgcn_readlane((int)c, (int)u0);
+    const uint32_t into = (t - ex * n_ff) / cu;   // pairs of u0 before t
+    return u0 * n_ff + min(into, n_ff);
+}
+
 // Producer: issue pairs [p0, p1) of the block (gate rows then up rows per
 // chunk).  idv holds expert id u in lane u.
 template <uint32_t UNIT>
@@ -621,7 +646,7 @@ __device__ inline void gu_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
         }
     };
     auto items = [&](uint32_t c) { return min(ch, np - c * ch); };
-    produce(Y, P->ends[wave], wave, C, S, issued, issue, items
+    produce(Y, P->ends[wave], wave, C, S, a.ahead, issued, issue, items
 #ifdef Q4MI_TRACE
             , a.trace, 0
 #endif
@@ -785,7 +810,14 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     }
     const uint32_t nu = uniq ? a.src.n_fixed : P->nu;
     const uint32_t PT = nu * a.n_ff;
-    const uint32_t p0 = share_lo(PT, bid, nblk), p1 = share_lo(PT, bid + 1, nblk);
+    uint32_t p0, p1;
+    if (NT == 1 || uniq) {
+        p0 = share_lo(PT, bid, nblk);
+        p1 = share_lo(PT, bid + 1, nblk);
+    } else {   // shares of equal work: an expert picked by more tokens costs more
+        p0 = share_weighted(P, nu, a.n_ff, bid, nblk, lane);
+        p1 = share_weighted(P, nu, a.n_ff, bid + 1, nblk, lane);
+    }
 
     if (wave < kProd) {
         // every expert id in one register (lane u holds id u): a segment's id
@@ -837,7 +869,7 @@ __device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
         }
     };
     auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
-    produce(Y, P->ends[wave], wave, C, S, issued, issue, items
+    produce(Y, P->ends[wave], wave, C, S, a.ahead, issued, issue, items
 #ifdef Q4MI_TRACE
             , a.trace, 1
 #endif
