@@ -371,6 +371,8 @@ def main():
     del g_full, g_gu, g_dn, arenas
     torch.cuda.empty_cache()
 
+    if not args.no_extra:
+        out["decode_floors"] = bench_floors(M, torch, q4mi)
     if not args.no_prefill:
         out["mfma_peak"] = bench_mfma_peak(M, torch, q4mi)
         out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
@@ -392,6 +394,54 @@ def main():
         out["cpu_baselines"] = cpu_baselines(facts)
     sys.stdout.write(json.dumps(out) + "\n")
     sys.stdout.flush()
+
+
+def bench_floors(M, torch, q4mi, n=48, reps=20):
+    """Floors of the decode kernels' structure on this GPU (measurement
+    build's stream probe, one 1024-thread block per CU as moe_gu_k /
+    moe_dn_k): a graph of n back-to-back launches, each streaming its own
+    per-CU share into LDS from distinct memory (beyond the Infinity Cache);
+    per-launch time = graph time / n."""
+    import ctypes
+    P = q4mi.ptr
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    res = {"n_cu": cus, "launches_per_graph": n}
+    per_cases = [(0, 4), (20 * 1024, 4), (40 * 1024, 4), (60 * 1024, 4), (140 * 1024, 4),
+                 (140 * 1024, 8)]
+    src = torch.empty(n * cus * 140 * 1024, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    for per, waves in per_cases:
+        b = ctypes.c_uint64(0)
+
+        def launches():
+            for i in range(n):
+                q4mi.check(M.q4mi_stream_probe(P(src) + i * cus * per, per, waves,
+                                               ctypes.byref(b)), "stream probe", M)
+        launches()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            q4mi.use_torch_stream(M)
+            launches()
+        q4mi.use_torch_stream(M)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / (reps * n)
+        key = "empty" if not per else "%dKB_per_cu_%dwaves" % (per // 1024, waves)
+        res[key] = {"us_per_launch": round(t * 1e6, 2)}
+        if per:
+            res[key]["MB"] = round(b.value / 1e6, 2)
+            res[key]["GB/s"] = round(b.value / t / 1e9, 1)
+        del g
+    del src
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_mfma_peak(L, torch, q4mi, iters=16384, reps=5):

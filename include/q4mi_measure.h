@@ -26,6 +26,12 @@ void q4mi_moe_lds_cap(uint32_t bytes);
  * int8 32x32x32, 1: fp16 32x32x16); *ops = the launch's ops, for a
  * caller-timed rate. */
 bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops);
+/* One launch of the stream floor probe: one 1024-thread block per CU whose
+ * `waves` producer waves copy per_block bytes (src + block * per_block)
+ * into LDS with 1 KB global_load_lds_dwordx4 operations and wait for them;
+ * per_block = 0 launches the same grid empty.  *bytes = the launch's
+ * total.  The floors of the decode kernels' structure. */
+bool q4mi_stream_probe(const void *src, uint32_t per_block, uint32_t waves, uint64_t *bytes);
 
 #ifdef __cplusplus
 }

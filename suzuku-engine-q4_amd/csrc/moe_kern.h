@@ -1241,6 +1241,9 @@ static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
 // 96 teams cover a block's (expert, row) items in one round; else the row
 // layout.
 static RowLayout dn_layout(uint32_t G, int NT) {
+    // 8 lanes x 2 groups: a one-token block's 88 items in one round of 96
+    // teams.  (4 lanes x 4 groups for windows measured slower: 36.0 against
+    // 35.1 us for 4 tokens.)
     if (G == 16 && NT <= 4) return RowLayout{8, 2};
     return layout_for(G);
 }

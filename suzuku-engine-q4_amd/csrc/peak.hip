@@ -66,6 +66,26 @@ __global__ __launch_bounds__(256) void mfma_peak_k(uint32_t iters, float *__rest
 static float *g_sink = nullptr;
 static uint32_t g_sink_n = 0;
 
+// Floor probes of the decode kernels' structure (one 1024-thread block per
+// CU, as moe_gu_k / moe_dn_k): `waves` producer waves of each block copy the
+// block's `per_block` bytes (contiguous, at src + block * per_block) into LDS
+// with 1 KB global_load_lds_dwordx4 operations, then wait for them; the
+// other waves exit.  per_block = 0: an empty kernel of the same shape.
+__global__ __launch_bounds__(1024) void stream_probe_k(const uint8_t *__restrict__ src,
+                                                       uint32_t per_block, uint32_t waves) {
+    extern __shared__ __align__(16) uint8_t sm[];
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (w >= waves || !per_block) return;
+    const uint8_t *s = src + (size_t)blockIdx.x * per_block;
+    const uint32_t nops = per_block / 1024, base = (uint32_t)(uintptr_t)sm;
+    for (uint32_t j = w; j < nops; j += waves) {
+        const uint32_t lds = __builtin_amdgcn_readfirstlane(base + (j % 150u) * 1024u);
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :: "v"(s + (size_t)j * 1024 + lane * 16), "s"(lds) : "memory", "m0");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 }  // namespace q4mi
 
 using namespace q4mi;
@@ -76,6 +96,33 @@ extern "C" {
  * throughput probe on the library stream; kind 0 = int8 32x32x32, 1 = fp16
  * 32x32x16.  *ops receives the launch's integer ops / flops, so that the
  * caller's timing of the launch gives the rate. */
+/* Measurement hook: one launch of the stream floor probe (one 1024-thread
+ * block per CU, `waves` producer waves copying per_block bytes each into LDS;
+ * per_block = 0: empty kernel).  src must hold cu_count() * per_block bytes;
+ * *bytes = the launch's total. */
+bool q4mi_stream_probe(const void *src, uint32_t per_block, uint32_t waves, uint64_t *bytes) {
+    if ((per_block && !src) || per_block % 1024 || per_block > 150u * 1024 || !waves ||
+        waves > 16 || !bytes) {
+        set_error("q4mi_stream_probe: bad arguments");
+        return false;
+    }
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *)stream_probe_k,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                150 * 1024) != hipSuccess) {
+            set_error("q4mi_stream_probe: LDS limit");
+            return false;
+        }
+        attr = true;
+    }
+    const uint32_t blocks = (uint32_t)cu_count();
+    *bytes = (uint64_t)blocks * per_block;
+    stream_probe_k<<<dim3(blocks), dim3(1024), 150 * 1024, stream()>>>((const uint8_t *)src,
+                                                                       per_block, waves);
+    return launch_ok("stream_probe_k");
+}
+
 bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops) {
     if ((kind != 0 && kind != 1) || !iters || !ops) {
         set_error("q4mi_mfma_probe: bad arguments");

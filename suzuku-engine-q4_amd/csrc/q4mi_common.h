@@ -180,13 +180,14 @@ __device__ inline float q4mi_sum_width(float v) {
     return v;
 }
 
-// DPP reduction over aligned groups of W lanes (W = 8, 16, 32, 64); the
+// DPP reduction over aligned groups of W lanes (W = 4, 8, 16, 32, 64); the
 // group's total lands in its last lane (lane % W == W-1).
 template <int W>
 __device__ inline float q4mi_rsum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xF, 0xF, true));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xF, 0xF, true));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
+    if (W >= 8)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
     if (W >= 16)
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xF, 0xF, true));
     if (W >= 32)

@@ -115,6 +115,7 @@ _MEAS_SIGS = {
     "q4mi_moe_phases": (None, [_c.c_int]),
     "q4mi_moe_lds_cap": (None, [_u32]),
     "q4mi_mfma_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
+    "q4mi_stream_probe": (_c.c_bool, [_vp, _u32, _u32, _c.POINTER(_c.c_uint64)]),
 }
 
 _lib = None
