@@ -235,7 +235,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--profile", choices=["decode", "window", "prefill"],
+                    help="a short run of one workload for rocprofv3 (no CPU baseline)")
     args = ap.parse_args()
+    if args.profile:
+        args.no_cpu = True
+        args.no_prefill = args.profile != "prefill"
+        args.no_extra = args.profile != "window"
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the routed-expert path is a "
               "single-GPU kernel set; multi-GPU sharding is a design note, not built).",
@@ -366,12 +372,13 @@ def main():
     if not args.no_extra:
         out["config3_window"] = bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
                                              capture, timed, args)
-        out["config2_routed"] = bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
-                                             capture, timed, args)
+        if not args.profile:
+            out["config2_routed"] = bench_routed(L, torch, np, q4mi, arenas, stride, og, ou,
+                                                 od, NL, capture, timed, args)
     del g_full, g_gu, g_dn, arenas
     torch.cuda.empty_cache()
 
-    if not args.no_extra:
+    if not args.no_extra and not args.profile:
         out["decode_floors"] = bench_floors(M, torch, q4mi)
     if not args.no_prefill:
         out["mfma_peak"] = bench_mfma_peak(M, torch, q4mi)
@@ -379,7 +386,7 @@ def main():
         out["prefill"]["pct_of_measured_int8_peak"] = round(
             100 * out["prefill"]["mmq_TOPS"] / out["mfma_peak"]["int8_TOPS"], 2)
         out["prefill_xg"] = bench_prefill_xg(L, torch, np, q4mi, synth, args)
-    if not args.no_extra:
+    if not args.no_extra and not args.profile:
         out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1,
                                          "configs[0]")
         out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936,
