@@ -69,12 +69,12 @@ __device__ inline int group_sum(const WGroup &w, const int32_t (&q)[8]) {
         for (int k = 0; k < 4; k++) a = q4mi_sdot4(w.w[k], q[k], a);
 #pragma unroll
         for (int k = 4; k < 8; k++) b = q4mi_sdot4(w.w[k], q[k], b);
-        return a * w.m1 + b * w.m2;
+        return __mul24(a, w.m1) + __mul24(b, w.m2);
     } else {
         int s = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) s = q4mi_sdot4(w.w[k], q[k], s);
-        return s * w.m1;
+        return __mul24(s, w.m1);
     }
 }
 

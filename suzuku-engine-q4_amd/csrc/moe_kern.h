@@ -359,7 +359,8 @@ __device__ inline void group_w(const uint32_t *stab, const uint8_t *lb, const ui
     }
 }
 
-// Exact group sum of one token: m1 * quads 0-3 + m2 * quads 4-7.
+// Exact group sum of one token: m1 * quads 0-3 + m2 * quads 4-7 (24-bit
+// multiplies, full rate: |sums| < 2^20, |multipliers| <= 2^7).
 template <uint32_t TY>
 __device__ inline int tsum(const int32_t (&w)[8], const int32_t (&q)[8], int m1, int m2) {
     if constexpr (two_mult<TY>()) {
@@ -368,12 +369,12 @@ __device__ inline int tsum(const int32_t (&w)[8], const int32_t (&q)[8], int m1,
         for (int k = 0; k < 4; k++) a = q4mi_sdot4(w[k], q[k], a);
 #pragma unroll
         for (int k = 4; k < 8; k++) b = q4mi_sdot4(w[k], q[k], b);
-        return a * m1 + b * m2;
+        return __mul24(a, m1) + __mul24(b, m2);
     } else {
         int s = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) s = q4mi_sdot4(w[k], q[k], s);
-        return s * m1;
+        return __mul24(s, m1);
     }
 }
 
@@ -741,7 +742,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
                         int32_t wa[8], wb[8];
                         int ma, mb;
                         float d;
-                        iq3s_group2(stab, tile, tw, (which * ch + j) * rb, g, wa, wb, ma, mb, d);
+                        iq3s_group2(stab, tile, tw, __umul24(which * ch + j, rb), g, wa, wb, ma, mb, d);
                         dot(m, which, wa, ma, ma, d);
                         dot(m + 1, which, wb, mb, mb, d);
                     }
@@ -755,7 +756,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
                         int32_t w[8];
                         int mult, mult2;
                         float d;
-                        group_w<TY>(stab, tile, tw, (which * ch + j) * rb, g, w, mult, mult2, d);
+                        group_w<TY>(stab, tile, tw, __umul24(which * ch + j, rb), g, w, mult, mult2, d);
                         dot(m, which, w, mult, mult2, d);
                     }
                 }
@@ -967,7 +968,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
                     int32_t wa[8], wb[8];
                     int ma, mb;
                     float d;
-                    iq3s_group2(stab, tile, tw, jj * rb, g, wa, wb, ma, mb, d);
+                    iq3s_group2(stab, tile, tw, __umul24(jj, rb), g, wa, wb, ma, mb, d);
                     dot(g, wa, ma, ma, d);
                     dot(g + 1, wb, mb, mb, d);
                 }
@@ -978,7 +979,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
                     int32_t w[8];
                     int mult, mult2;
                     float d;
-                    group_w<TY>(stab, tile, tw, jj * rb, g, w, mult, mult2, d);
+                    group_w<TY>(stab, tile, tw, __umul24(jj, rb), g, w, mult, mult2, d);
                     dot(g, w, mult, mult2, d);
                 }
             }
