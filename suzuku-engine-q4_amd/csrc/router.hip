@@ -64,14 +64,13 @@ __global__ __launch_bounds__(256) void router_gemv_k(const uint8_t *__restrict__
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t t0 = blockIdx.y * TT, nt = min(TT, n_tok - t0);
     const uint32_t q4 = K / 4;
-    for (uint32_t i = threadIdx.x; i < nt * q4; i += 256)
-        ((float4 *)xs)[i] = ((const float4 *)(x + (size_t)t0 * K))[i];
-    __syncthreads();
     const uint32_t rows = n_exp + (sgw ? 1u : 0u);
     const uint32_t ni = K / 256;
     const size_t rb = (size_t)K * (WT == kRtF32 ? 4 : 2);
-    for (uint32_t r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {
-        float4 wv[kRtMaxNI];
+    // this wave's first row is loaded before the block stages x, so the two
+    // memory round trips overlap
+    float4 wv[kRtMaxNI];
+    auto load_row = [&](uint32_t r) __attribute__((always_inline)) {
         const bool gate = r == n_exp;
 #pragma unroll
         for (uint32_t i = 0; i < kRtMaxNI; i++) {
@@ -79,6 +78,15 @@ __global__ __launch_bounds__(256) void router_gemv_k(const uint8_t *__restrict__
                 wv[i] = gate ? ((const float4 *)sgw)[64 * i + lane]
                              : load_w4<WT>(w + (size_t)r * rb, 64 * i + lane);
         }
+    };
+    const uint32_t r0 = blockIdx.x * 4 + wave;
+    if (r0 < rows) load_row(r0);
+    for (uint32_t i = threadIdx.x; i < nt * q4; i += 256)
+        ((float4 *)xs)[i] = ((const float4 *)(x + (size_t)t0 * K))[i];
+    __syncthreads();
+    for (uint32_t r = r0; r < rows; r += gridDim.x * 4) {
+        const bool gate = r == n_exp;
+        if (r != r0) load_row(r);
         for (uint32_t t = 0; t < nt; t++) {
             const float4 *xt = (const float4 *)(xs + (size_t)t * K);
             float acc = 0.f;
