@@ -401,9 +401,6 @@ def main():
         out["cpu_baselines"] = cpu_baselines(facts)
     sys.stdout.write(json.dumps(out) + "\n")
     sys.stdout.flush()
-    # leave at once: nothing else to release, and no exit handler may linger
-    # after the result is out
-    os._exit(0)
 
 
 def bench_floors(M, torch, q4mi, n=48, reps=20):
