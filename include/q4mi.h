@@ -221,8 +221,9 @@ bool q4_hip_expert_reduce(float *d_y, const float *d_pd, const int32_t *d_rsrc,
 /* ------------------------------------------------------------ prefill MMQ */
 
 /* Replaces the q4_mmq_* wrapper around vendored ggml MMQ
- * (src/q4.h:1150-1175, src/q4_mmq.cu:250-610).  Types IQ3_S, Q8_0;
- * w_rows % 128 == 0, w_cols % 256 == 0 (IQ3_S: % 512, whole-dword rows).  Weight buffers must be readable up
+ * (src/q4.h:1150-1175, src/q4_mmq.cu:250-610).  Types IQ3_S, Q8_0, IQ4_NL,
+ * Q2_0, IQ2_S; w_rows % 128 == 0, w_cols % 256 == 0 with whole-dword rows
+ * (IQ3_S: w_cols % 512).  Weight buffers must be readable up
  * to the next 4-byte boundary after their last byte (any hipMalloc'd
  * buffer is).  The activation buffer layout is this
  * library's (q4_mmq_q8_bytes gives its size); its codes are the bit-exact

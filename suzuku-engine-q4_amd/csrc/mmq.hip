@@ -26,6 +26,7 @@
 
 #include <algorithm>
 
+#include "formats.h"
 #include "q4mi_common.h"
 #include "q4mi_internal.h"
 
@@ -156,11 +157,39 @@ constexpr int MMQ_MB = 128;      // token rows per block
 //          one wave decodes at a common byte offset fall on 32 banks, and
 //          one 58-lane copy fills two whole rows.
 //   Q8_0:  the dwords rounded to an even count, copied as one linear run.
+//   IQ4_NL, Q2_0, IQ2_S: like Q8_0 (8 x 18, 4 x 18 and 82 bytes per 256).
 template <uint32_t TY>
 struct RawSpec {
-    static constexpr uint32_t SB = TY == Q4MI_T_IQ3_S ? 110u : 8u * 34u;  // bytes / 256 values
+    static constexpr uint32_t SB = TY == Q4MI_T_IQ3_S    ? 110u
+                                   : TY == Q4MI_T_Q8_0   ? 8u * 34u
+                                   : TY == Q4MI_T_IQ4_NL ? 8u * 18u
+                                   : TY == Q4MI_T_Q2_0   ? 4u * 18u
+                                                         : 82u;   // IQ2_S
     static constexpr uint32_t SS = TY == Q4MI_T_IQ3_S ? 29u * 4u
                                                       : ((SB + 2u + 3u) / 4u + 1u) / 2u * 8u;
+};
+
+// Per-format facts of the MMQ operand decode:
+//   kSuper  the block scale is per superblock (IQ3_S, IQ2_S: the exact group
+//           sums times d_x accumulate in `inner`, times d_w once per
+//           superblock), else per 32 or 64 values (d_w folded per group);
+//   kTab    entries of the LDS decode table g16 (IQ3_S: codebook as fp16
+//           magnitudes; IQ2_S: codebook bytes; IQ4_NL: byte -> fp16 values of
+//           its two nibbles; Q2_0: byte -> its four fp16 values c - 1).
+template <uint32_t TY>
+struct MmqFmt {
+    static constexpr bool kSuper = TY == Q4MI_T_IQ3_S || TY == Q4MI_T_IQ2_S;
+    static constexpr uint32_t kTab = TY == Q4MI_T_IQ3_S    ? 512u
+                                     : TY == Q4MI_T_IQ2_S  ? 1024u
+                                     : TY == Q4MI_T_IQ4_NL ? 256u
+                                     : TY == Q4MI_T_Q2_0   ? 256u
+                                                           : 1u;
+    // byte offset of group j's scale inside the superblock, and its factor
+    __device__ static inline uint32_t doff(uint32_t j) {
+        return TY == Q4MI_T_Q8_0 ? 34u * j : TY == Q4MI_T_IQ4_NL ? 18u * j
+             : TY == Q4MI_T_Q2_0 ? 18u * (j >> 1) : 0u;
+    }
+    static constexpr float kDScale = TY == Q4MI_T_IQ2_S ? 0.125f : 1.f;
 };
 
 // Double-buffered stages of 64 K values (two q8 groups).  Activation rows
@@ -173,7 +202,7 @@ struct MmqLds {
     _Float16 act[2][MMQ_MB][64];            // 32 KB; reused for the fused hand-off
     float dx[2][MMQ_MB][2];                 // group scales of each staged pair
     uint8_t raw[2][MMQ_NB][RawSpec<TY>::SS];  // raw weight bytes per superblock
-    uint2 g16[512];                         // IQ3_S grid as fp16 magnitudes
+    uint2 g16[MmqFmt<TY>::kTab];            // decode table (MmqFmt)
     uint2 sm16[16];                         // sign nibble -> fp16 sign masks
 };
 
@@ -215,7 +244,7 @@ constexpr float kXgWs = 256.f;
 template <uint32_t TY, bool XG = false>
 __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t j,
                                 uint32_t kh, half8_t &A0, half8_t &A1) {
-    if (TY == Q4MI_T_IQ3_S) {
+    if constexpr (TY == Q4MI_T_IQ3_S) {
         const uint32_t qa = lds_u16(R + 2 + 8 * j + 2 * kh);       // qs entries 2kh, 2kh+1
         const uint32_t qb = lds_u16(R + 2 + 8 * j + 4 + 2 * kh);   // 4+2kh, 5+2kh
         const uint32_t qh = R[66 + j];
@@ -241,6 +270,65 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
         }
         A0 = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
         A1 = __builtin_bit_cast(half8_t, make_uint4(o[4], o[5], o[6], o[7]));
+    } else if constexpr (TY == Q4MI_T_IQ4_NL) {
+        // block j: qs at 18j+2; values 8kh+k (low nibble of qs[8kh+k], in A0)
+        // and 16+8kh+k (its high nibble, in A1); the table gives both as fp16
+        const uint8_t *qs = R + 18 * j + 2 + 8 * kh;
+        uint32_t t[8];
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const uint32_t b2 = lds_u16(qs + k);
+            t[k] = L.g16[b2 & 0xffu].x;
+            t[k + 1] = L.g16[b2 >> 8].x;
+        }
+        uint32_t o0[4], o1[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o0[k] = __builtin_amdgcn_perm(t[2 * k + 1], t[2 * k], 0x05040100u);
+            o1[k] = __builtin_amdgcn_perm(t[2 * k + 1], t[2 * k], 0x07060302u);
+        }
+        A0 = __builtin_bit_cast(half8_t, make_uint4(o0[0], o0[1], o0[2], o0[3]));
+        A1 = __builtin_bit_cast(half8_t, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+    } else if constexpr (TY == Q4MI_T_Q2_0) {
+        // group j = half j&1 of block j>>1; code byte b holds values 4b..4b+3:
+        // A0 = bytes 2kh, 2kh+1; A1 = bytes 4+2kh, 5+2kh
+        const uint8_t *cs = R + 18 * (j >> 1) + 2 + 8 * (j & 1u);
+        const uint32_t a = lds_u16(cs + 2 * kh), b = lds_u16(cs + 4 + 2 * kh);
+        const uint2 t0 = L.g16[a & 0xffu], t1 = L.g16[a >> 8];
+        const uint2 t2 = L.g16[b & 0xffu], t3 = L.g16[b >> 8];
+        A0 = __builtin_bit_cast(half8_t, make_uint4(t0.x, t0.y, t1.x, t1.y));
+        A1 = __builtin_bit_cast(half8_t, make_uint4(t2.x, t2.y, t3.x, t3.y));
+    } else if constexpr (TY == Q4MI_T_IQ2_S) {
+        // group j: grid entries l = 0..3 (8 values each), index qs[4j+l] with
+        // 2 bits of qh[j]; A0 = entry kh (multiplier of values 0-15), A1 =
+        // entry 2+kh (values 16-31).  Magnitude bytes become fp16 as
+        // 1024 + b (exponent bits 0x64) minus 1024, exactly.
+        const uint32_t qs4 = lds_u16(R + 2 + 4 * j) | (lds_u16(R + 4 + 4 * j) << 16);
+        const uint32_t sg4 = lds_u16(R + 34 + 4 * j) | (lds_u16(R + 36 + 4 * j) << 16);
+        const uint32_t qh = R[66 + j], sc = R[74 + j];
+        const half2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
+        auto entry = [&](uint32_t l, uint32_t mult, half8_t &A) __attribute__((always_inline)) {
+            const uint32_t idx = ((qs4 >> (8 * l)) & 0xffu) | ((qh << (8 - 2 * l)) & 0x300u);
+            const uint2 g = L.g16[idx];
+            const uint32_t sg = (sg4 >> (8 * l)) & 0xffu;
+            const uint2 m0 = L.sm16[sg & 15u], m1 = L.sm16[sg >> 4];
+            const half2_t mm = {(_Float16)(float)mult, (_Float16)(float)mult};
+            const uint32_t w[4] = {g.x, g.x, g.y, g.y};
+            const uint32_t sel[2] = {0x04010400u, 0x04030402u};
+            const uint32_t msk[4] = {m0.x, m0.y, m1.x, m1.y};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                half2_t v = __builtin_bit_cast(half2_t,
+                                               __builtin_amdgcn_perm(0x64646464u, w[k], sel[k & 1]));
+                v = v + off;
+                v = __builtin_bit_cast(half2_t, __builtin_bit_cast(uint32_t, v) ^ msk[k]) * mm;
+                o[k] = __builtin_bit_cast(uint32_t, v);
+            }
+            A = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+        };
+        entry(kh, 2u * (sc & 15u) + 1u, A0);
+        entry(2 + kh, 2u * (sc >> 4) + 1u, A1);
     } else {
         // Q8_0 block j of the superblock: qs at 34j+2; values 8kh.. and 16+8kh..
         const uint8_t *qs = R + 34 * j + 2;
@@ -425,7 +513,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     }
     const uint32_t arow = 32 * wv + (lane & 31u);    // this lane's weight row in the tile
     issue_stage(0);
-    if (TY == Q4MI_T_IQ3_S) {   // IQ3_S tables (read after the first barrier pair)
+    if constexpr (TY == Q4MI_T_IQ3_S) {   // tables (read after the first barrier pair)
 #pragma unroll
         for (int h2 = 0; h2 < 2; h2++) {
             const uint32_t c = code[h2];
@@ -437,12 +525,39 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             }
             L.g16[tid + 256 * h2] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }
-        if (tid < 16) {
-            uint32_t sgn[4];
+    }
+    if constexpr (TY == Q4MI_T_IQ2_S) {   // codebook magnitude bytes
+        for (uint32_t i = tid; i < 1024; i += 256) {
+            const uint32_t c = q4mi_iq2s_code_dev[i];
+            uint32_t lo = 0, hi = 0;
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) sgn[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
-            L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
+            for (int jj = 0; jj < 4; jj++) {
+                const uint32_t x0 = (c >> (2 * jj)) & 3u, x1 = (c >> (2 * jj + 8)) & 3u;
+                lo |= (x0 == 0 ? 8u : x0 == 1 ? 25u : 43u) << (8 * jj);
+                hi |= (x1 == 0 ? 8u : x1 == 1 ? 25u : 43u) << (8 * jj);
+            }
+            L.g16[i] = make_uint2(lo, hi);
         }
+    }
+    if constexpr (TY == Q4MI_T_IQ4_NL) {   // byte -> fp16 of both nibbles' values
+        constexpr int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                   1,    13,   25,  38,  53,  69,  89,  113};
+        const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(float)kv[tid & 15u]);
+        const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(float)kv[tid >> 4]);
+        L.g16[tid] = make_uint2(lo | (hi << 16), 0u);
+    }
+    if constexpr (TY == Q4MI_T_Q2_0) {   // byte -> its four fp16 values c - 1
+        uint32_t h[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+            h[jj] = __builtin_bit_cast(uint16_t, (_Float16)(float)((int)((tid >> (2 * jj)) & 3u) - 1));
+        L.g16[tid] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    }
+    if (MmqFmt<TY>::kSuper && tid < 16) {   // sign nibble -> fp16 sign masks
+        uint32_t sgn[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) sgn[jj] = ((tid >> jj) & 1u) ? 0x8000u : 0u;
+        L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
     }
     for (uint32_t s = 0; s < nst; s++) {
         const uint32_t sbi = s >> 2, q = s & 3u;
@@ -494,7 +609,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         };
         auto scale = [&](int n, const f32x16_t &sacc, float dxv) __attribute__((always_inline)) {
             const int gl = n / NSUB, t = n % NSUB;
-            if (TY == Q4MI_T_IQ3_S) {
+            if constexpr (MmqFmt<TY>::kSuper) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
             } else {
@@ -502,7 +617,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const uint32_t nr = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                    const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][nr][roff] + 34 * j));
+                    const float dw = q4mi_h2f(
+                        lds_u16(&L.raw[sbi & 1u][nr][roff] + MmqFmt<TY>::doff(j)));
                     acc[t][i] = fmaf(sacc[i], dxv * dw, acc[t][i]);
                 }
             }
@@ -532,11 +648,12 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             cur = nxt;
             dcur = dnext;
         }
-        if (TY == Q4MI_T_IQ3_S && q == 3) {   // superblock done: acc += inner * d_w
+        if (MmqFmt<TY>::kSuper && q == 3) {   // superblock done: acc += inner * d_w
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
-                const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][roff]));
+                const float dw = q4mi_h2f(lds_u16(&L.raw[sbi & 1u][n][roff])) *
+                                 MmqFmt<TY>::kDScale;
 #pragma unroll
                 for (int t = 0; t < NSUB; t++) {
                     acc[t][i] = fmaf(inner[t][i], dw, acc[t][i]);
@@ -681,8 +798,13 @@ static bool ensure_tiles(uint32_t n) {
     return true;
 }
 
+static bool mmq_type(uint32_t ty) {
+    return ty == Q4MI_T_IQ3_S || ty == Q4MI_T_Q8_0 || ty == Q4MI_T_IQ4_NL || ty == Q4MI_T_Q2_0 ||
+           ty == Q4MI_T_IQ2_S;
+}
+
 bool mmq_supported(uint32_t ty, uint64_t w_rows, uint64_t w_cols) {
-    if (ty != Q4MI_T_IQ3_S && ty != Q4MI_T_Q8_0) return false;
+    if (!mmq_type(ty)) return false;
     // rows must be 4-byte multiples (IQ3_S: an even number of superblocks)
     return w_rows > 0 && w_rows % MMQ_NB == 0 && w_cols > 0 && w_cols % 256 == 0 &&
            w_cols <= 65536 && q4mi_row_bytes(ty, w_cols) % 4 == 0;
@@ -799,12 +921,22 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.hd = hq ? (float *)((uint8_t *)hq + total_rows * a.n_ff * 2) : nullptr;
     if (hq) {
         const dim3 grid((uint32_t)(a.n_ff / 64), max_tiles);
-        return ty == Q4MI_T_IQ3_S ? mmq_launch<Q4MI_T_IQ3_S, true>(a, grid)
-                                  : mmq_launch<Q4MI_T_Q8_0, true>(a, grid);
+        switch (ty) {
+        case Q4MI_T_IQ3_S: return mmq_launch<Q4MI_T_IQ3_S, true>(a, grid);
+        case Q4MI_T_Q8_0: return mmq_launch<Q4MI_T_Q8_0, true>(a, grid);
+        case Q4MI_T_IQ2_S: return mmq_launch<Q4MI_T_IQ2_S, true>(a, grid);
+        case Q4MI_T_IQ4_NL: return mmq_launch<Q4MI_T_IQ4_NL, true>(a, grid);
+        default: return mmq_launch<Q4MI_T_Q2_0, true>(a, grid);
+        }
     }
     const dim3 grid((uint32_t)(w_rows / MMQ_NB), max_tiles);
-    return ty == Q4MI_T_IQ3_S ? mmq_launch<Q4MI_T_IQ3_S, false>(a, grid)
-                              : mmq_launch<Q4MI_T_Q8_0, false>(a, grid);
+    switch (ty) {
+    case Q4MI_T_IQ3_S: return mmq_launch<Q4MI_T_IQ3_S, false>(a, grid);
+    case Q4MI_T_Q8_0: return mmq_launch<Q4MI_T_Q8_0, false>(a, grid);
+    case Q4MI_T_IQ2_S: return mmq_launch<Q4MI_T_IQ2_S, false>(a, grid);
+    case Q4MI_T_IQ4_NL: return mmq_launch<Q4MI_T_IQ4_NL, false>(a, grid);
+    default: return mmq_launch<Q4MI_T_Q2_0, false>(a, grid);
+    }
 }
 
 bool swiglu_launch(const float *gu, float *h, uint64_t rows, uint64_t n_ff) {
@@ -846,7 +978,7 @@ uint32_t q4_mmq_group(void) {
 
 /* A tile exists for (type, w_rows): IQ3_S or Q8_0, w_rows % 128 == 0. */
 bool q4_mmq_supported(uint32_t type, uint64_t w_rows) {
-    return (type == Q4MI_T_IQ3_S || type == Q4MI_T_Q8_0) && w_rows > 0 && w_rows % MMQ_NB == 0;
+    return mmq_type(type) && w_rows > 0 && w_rows % MMQ_NB == 0;
 }
 
 /* Bytes of the activation buffer q4_mmq_quantize fills for rows x cols:

@@ -136,3 +136,79 @@ def test_format_coverage_rules(gpu):
     assert gpu.q4_hip_moe_win_ok(T_IQ2_S, T_IQ2_S, T_Q2_0, 2048, 512, 4)
     assert not gpu.q4_hip_moe_win_ok(T_IQ4_NL, T_IQ4_NL, T_IQ3_S, 2048, 512, 4)
     assert not gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, T_Q6_K, 2048, 512, 4)
+
+
+def mmq_q8(L, x, rows_idx, K):
+    import torch
+    xq = torch.zeros(int(L.q4_mmq_q8_bytes(len(rows_idx), K)), dtype=torch.uint8, device="cuda")
+    q4mi.check(L.q4_mmq_quantize(q4mi.ptr(dev(x)), q4mi.ptr(dev(np.asarray(rows_idx, np.int32))),
+                                 q4mi.ptr(xq), 21, K, len(rows_idx)), "q4_mmq_quantize")
+    return xq
+
+
+@pytest.mark.parametrize("ty,N,K", [(T_IQ4_NL, 2048, 512), (T_Q2_0, 2048, 512),
+                                    (T_IQ2_S, 1024, 2048), (T_IQ2_S, 2048, 512),
+                                    (T_IQ4_NL, 256, 2048)])
+def test_mmq_formats_mul_id(gpu, oracle, ty, N, K):
+    """The prefill MMQ over the other formats, ragged experts (empty, tile
+    edges, single rows), against the oracle's int8 row dot."""
+    import torch
+    rng = np.random.default_rng(ty * 7 + N + K)
+    per = [70, 0, 1, 129, 5, 33]
+    E = len(per)
+    rb = om.row_bytes(ty, K)
+    W = synth.matrix(rng, ty, E * N, K)
+    T = 200
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    a_tok = np.concatenate([rng.integers(0, T, n) for n in per]).astype(np.int32)
+    bounds = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+    total = int(bounds[-1])
+    assert gpu.q4_mmq_supported(ty, N)
+    xq = mmq_q8(gpu, x, a_tok, K)
+    dst = torch.zeros((total, N), dtype=torch.float32, device="cuda")
+    q4mi.check(gpu.q4_mmq_mul_id(q4mi.ptr(dev(W)), ty, N, K, N * rb, E, q4mi.ptr(xq),
+                                 q4mi.ptr(dev(bounds)), 0, total, q4mi.ptr(dst), N),
+               "q4_mmq_mul_id")
+    d = host(dst)
+    for e in range(E):
+        if per[e] == 0:
+            continue
+        rows = a_tok[bounds[e]:bounds[e + 1]]
+        ref = oracle.dot8_rows(ty, W[e * N * rb:(e + 1) * N * rb], N, K, x[rows])
+        assert rel_err(d[bounds[e]:bounds[e + 1]], ref) <= TOL, e
+
+
+def test_mmq_iq2s_gate_up_fused(gpu, oracle):
+    """Fused gate/up (SwiGLU + q8(h)) over IQ2_S experts: the q8(h) codes
+    against or_quant8 of the oracle's h (at most 1e-4 of them differ: h
+    rounding near a q8 boundary)."""
+    import torch
+    rng = np.random.default_rng(91)
+    H, F = 2048, 512
+    per = [40, 3, 0, 130]
+    E = len(per)
+    rb = om.row_bytes(T_IQ2_S, H)
+    W = synth.matrix(rng, T_IQ2_S, E * 2 * F, H)      # per expert: gate rows then up rows
+    T = 150
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    a_tok = np.concatenate([rng.integers(0, T, n) for n in per]).astype(np.int32)
+    bounds = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+    rows = int(bounds[-1])
+    xq = mmq_q8(gpu, x, np.arange(T), H)
+    hq = torch.zeros(int(gpu.q4_mmq_q8_bytes(rows, F)), dtype=torch.uint8, device="cuda")
+    q4mi.check(gpu.q4mi_mmq_gate_up(q4mi.ptr(dev(W)), T_IQ2_S, F, H, 2 * F * rb, E, q4mi.ptr(xq),
+                                    T, q4mi.ptr(dev(a_tok)), q4mi.ptr(dev(bounds)), rows,
+                                    q4mi.ptr(hq)), "gate_up")
+    hb = host(hq)
+    codes = hb[:rows * F * 2].view(np.float16).reshape(rows, F).astype(np.int32)
+    diff = 0
+    for e in range(E):
+        if not per[e]:
+            continue
+        Wg = W[e * 2 * F * rb:(e + 1) * 2 * F * rb]
+        gu = oracle.dot8_rows(T_IQ2_S, Wg, 2 * F, H, x[a_tok[bounds[e]:bounds[e + 1]]])
+        h = (gu[:, :F] / (1 + np.exp(-gu[:, :F].astype(np.float64))) * gu[:, F:]).astype(np.float32)
+        for i in range(per[e]):
+            q, _, _ = oracle.quant8(h[i])
+            diff += int(np.count_nonzero(q.astype(np.int32) != codes[bounds[e] + i]))
+    assert diff <= 1e-3 * rows * F, diff
