@@ -227,6 +227,7 @@ struct MmqArgs {
     uint64_t ld;
     _Float16 *hq;           // fused mode: [rows][n_ff] fp16 codes of h
     float *hd;              // fused mode: [rows][n_ff/32]
+    uint32_t wide;          // one- and two-sub-tile tiles use 256 / 128-value stages
 };
 
 __device__ inline uint32_t lds_u16(const uint8_t *p) { return *(const uint16_t *)p; }
@@ -391,7 +392,11 @@ __device__ inline void mmq_bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barri
 __device__ inline void mmq_bar_rd() { asm volatile("s_barrier" ::: "memory"); }
 
 // One (expert, weight block, token tile) of NSUB 32-row token sub-tiles.
-template <uint32_t TY, bool FUSED, int NSUB, bool XG = false>
+// KS = K values per stage: 64 for three or four token sub-tiles; one- and
+// two-sub-tile tiles take 256 / 128 (the same 16 KB of activation rows per
+// buffer), so their short per-stage compute waits for a memory round trip 4x
+// / 2x less often.
+template <uint32_t TY, bool FUSED, int NSUB, bool XG = false, uint32_t KS = 64>
 __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, uint8_t *smem,
                                                                const int4 tinfo) {
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
@@ -401,8 +406,17 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     // dword copies per superblock: IQ3_S two rows per copy, else linear
     constexpr uint32_t RAW_OPS = kIq ? MMQ_NB / 2 : (MMQ_NB * SSD + 63) / 64;
     constexpr uint32_t RAW_PER_WAVE = (RAW_OPS + 3) / 4;
+    constexpr uint32_t GPS = KS / 32;                         // q8 groups per stage
+    constexpr uint32_t SPS = 256 / KS;                        // stages per superblock
+    constexpr uint32_t RPO = 512 / KS;                        // activation rows per 1 KB copy
+    constexpr uint32_t CPR = KS / 8;                          // 16-byte chunks per row
+    constexpr uint32_t AOPS = NSUB * KS / 64;                 // activation copies per wave
+    static_assert(32 * NSUB * KS <= MMQ_MB * 64 && 32 * NSUB * GPS <= 2 * MMQ_MB, "stage fits");
     // copies per stage per wave: the activation rows and (q8 mode) their scales
-    constexpr uint32_t ST_OPS = NSUB + (XG ? 0 : 1);
+    constexpr uint32_t ST_OPS = AOPS + (XG ? 0 : 1);
+    _Float16 *const actb = &L.act[0][0][0];                   // [2][32 NSUB][KS] per buffer
+    float *const dxb = &L.dx[0][0][0];                        // [2][32 NSUB][GPS]
+    constexpr uint32_t kActBuf = MMQ_MB * 64, kDxBuf = MMQ_MB * 2;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kh = lane >> 5;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t e = (uint32_t)tinfo.x;
@@ -468,41 +482,43 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     issue_raw(0);   // needs only the expert: goes out before the activation rows resolve
 
     // source rows of this lane's copies: activation op m covers tile rows
-    // 8(wv + 4m) .. +7 (lane / 8 picks the row), the scale op rows 32wv..+31
-    // (rows past the tile's end copy the last row's bytes: their outputs are
-    // never stored, and the copy stays one instruction)
-    const _Float16 *arow_src[NSUB];
+    // RPO(wv + 4m) .. +RPO-1 (lane / CPR picks the row), the scale op the
+    // dwords 64wv .. 64wv+63 of the stage's [rows][GPS] scales (rows past
+    // the tile's end copy the last row's bytes: their outputs are never
+    // stored, and the copy stays one instruction)
+    const _Float16 *arow_src[AOPS];
 #pragma unroll
-    for (int m = 0; m < NSUB; m++) {
-        const uint32_t r = 8 * (wv + 4 * m) + lane / 8;
+    for (uint32_t m = 0; m < AOPS; m++) {
+        const uint32_t r = RPO * (wv + 4 * m) + lane / CPR;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
         const int64_t xr = a.act_row ? a.act_row[p] : p;
         arow_src[m] = a.xq + (uint64_t)xr * a.K;
     }
     const float *drow_src = nullptr;
     if constexpr (!XG) {
-        const uint32_t r = 32 * wv + lane / 2;
+        const uint32_t r = (64 * wv + lane) / GPS;
         const int32_t p = rbase + (int32_t)min(r, mrows - 1);
         const int64_t xr = a.act_row ? a.act_row[p] : p;
-        drow_src = a.xd + (uint64_t)xr * (a.K / 32);
+        drow_src = a.xd + (uint64_t)xr * (a.K / 32) + (64 * wv + lane) % GPS;
     }
     const uint32_t nsb = a.K / 256;
-    const uint32_t nst = 4 * nsb;                     // 64-value stages
+    const uint32_t nst = SPS * nsb;                   // KS-value stages
 
     // copies of stage s (activation codes + scales) into buffer s & 1
     auto issue_stage = [&](uint32_t s) __attribute__((always_inline)) {
         const uint32_t buf = s & 1u;
 #pragma unroll
-        for (int m = 0; m < NSUB; m++) {
-            const uint32_t j = wv + 4 * m;            // 8 rows per op
-            const uint32_t r = 8 * j + lane / 8;
-            const uint32_t c = (lane & 7u) ^ (r & 7u); // logical chunk stored at slot lane & 7
-            const _Float16 *src = arow_src[m] + s * 64 + c * 8;
-            mmq_copy<16>(src, mmq_lds(&L.act[buf][8 * j][0]));
+        for (uint32_t m = 0; m < AOPS; m++) {
+            const uint32_t j = wv + 4 * m;            // RPO rows per op
+            const uint32_t r = RPO * j + lane / CPR;
+            // logical chunk stored at slot lane % CPR (its low 3 bits
+            // swizzled by the row)
+            const uint32_t c = (lane % CPR) ^ (r & 7u);
+            const _Float16 *src = arow_src[m] + s * KS + c * 8;
+            mmq_copy<16>(src, mmq_lds(actb + buf * kActBuf + RPO * j * KS));
         }
         if constexpr (!XG) {
-            const float *dsrc = drow_src + s * 2 + (lane & 1u);
-            mmq_copy<4>(dsrc, mmq_lds(&L.dx[buf][32 * wv][0]));
+            mmq_copy<4>(drow_src + s * GPS, mmq_lds(dxb + buf * kDxBuf + 64 * wv));
         }
     };
     f32x16_t acc[NSUB], inner[NSUB];
@@ -560,7 +576,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         L.sm16[tid] = make_uint2(sgn[0] | (sgn[1] << 16), sgn[2] | (sgn[3] << 16));
     }
     for (uint32_t s = 0; s < nst; s++) {
-        const uint32_t sbi = s >> 2, q = s & 3u;
+        const uint32_t sbi = s / SPS, q = s % SPS;
         // the row's raw bytes start at the same offset inside its slot as
         // in memory (the slot begins at the enclosing dword)
         const uint32_t roff = (uint32_t)((uintptr_t)wsrc(0, sbi) & 3u);   // same for every row
@@ -569,14 +585,17 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         // LDS since stage 4 sbi - 3 (stage 0 waits for them below), and
         // their buffer is refilled only after the first barrier of stage
         // 4 sbi + 4.
-        half8_t A[2][2];
+        half8_t A[GPS][2];
         auto decode = [&]() __attribute__((always_inline)) {
             const uint8_t *R = &L.raw[sbi & 1u][arow][roff];
 #pragma unroll
-            for (int gl = 0; gl < 2; gl++)
-                decode_a<TY, XG>(L, R, 2 * q + gl, kh, A[gl][0], A[gl][1]);
+            for (uint32_t gl = 0; gl < GPS; gl++)
+                decode_a<TY, XG>(L, R, GPS * q + gl, kh, A[gl][0], A[gl][1]);
         };
-        if (s != 0) decode();
+        // (one stage per superblock: its raw bytes land only with this
+        // stage's wait, so the decode follows the barriers)
+        const bool ahead = SPS >= 2 && s != 0;
+        if (ahead) decode();
         // every wave is done with stage s-1 (and at a superblock start with
         // superblock sbi-1): their buffers may be refilled.  The reads in
         // flight here are the decode's, of a buffer nobody refills now.
@@ -592,18 +611,19 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         else mmq_wait<0>();
         mmq_bar();                                    // everyone's part is
         const uint32_t buf = s & 1u;
-        if (s == 0) decode();
+        if (!ahead) decode();
         // The stage's 2*NSUB products n = (group gl, token sub-tile t): an
         // exact-integer MFMA pair, then one scale FMA per output.  Product
         // n+1's pair is issued before product n's FMAs, so the FMAs never
         // wait on the pair right before them.
+        const _Float16 *actc = actb + buf * kActBuf;
         auto prod = [&](int n, float &dxo) __attribute__((always_inline)) {
             const int gl = n / NSUB, t = n % NSUB;
             const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
             const uint32_t tok = 32 * t + (lane & 31u);
-            const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
-            const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
-            dxo = L.dx[buf][tok][gl];
+            const half8_t B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
+            const half8_t B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
+            dxo = dxb[buf * kDxBuf + tok * GPS + gl];
             f32x16_t r = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, f32x16_t{}, 0, 0, 0);
             return __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, r, 0, 0, 0);
         };
@@ -613,7 +633,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
 #pragma unroll
                 for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
             } else {
-                const uint32_t j = 2 * q + gl;
+                const uint32_t j = GPS * q + gl;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const uint32_t nr = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
@@ -626,12 +646,12 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         if constexpr (XG) {
             // the MFMA accumulates across K straight into acc
 #pragma unroll
-            for (int n = 0; n < 2 * NSUB; n++) {
+            for (int n = 0; n < (int)GPS * NSUB; n++) {
                 const int gl = n / NSUB, t = n % NSUB;
                 const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;
                 const uint32_t tok = 32 * t + (lane & 31u);
-                const half8_t B0 = *(const half8_t *)&L.act[buf][tok][8 * (c0 ^ (tok & 7u))];
-                const half8_t B1 = *(const half8_t *)&L.act[buf][tok][8 * (c1 ^ (tok & 7u))];
+                const half8_t B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
+                const half8_t B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, acc[t], 0, 0, 0);
             }
@@ -640,15 +660,15 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         float dcur;
         f32x16_t cur = prod(0, dcur);
 #pragma unroll
-        for (int n = 0; n < 2 * NSUB; n++) {
+        for (int n = 0; n < (int)GPS * NSUB; n++) {
             float dnext = 0.f;
             f32x16_t nxt{};
-            if (n + 1 < 2 * NSUB) nxt = prod(n + 1, dnext);
+            if (n + 1 < (int)GPS * NSUB) nxt = prod(n + 1, dnext);
             scale(n, cur, dcur);
             cur = nxt;
             dcur = dnext;
         }
-        if (MmqFmt<TY>::kSuper && q == 3) {   // superblock done: acc += inner * d_w
+        if (MmqFmt<TY>::kSuper && q == SPS - 1) {   // superblock done: acc += inner * d_w
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const uint32_t n = 32 * wv + 8 * (i / 4) + 4 * kh + (i % 4);
@@ -776,8 +796,14 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
     case 4: mmq_tile<TY, FUSED, 4, XG>(a, smem, tinfo); break;
     case 3: mmq_tile<TY, FUSED, 3, XG>(a, smem, tinfo); break;
-    case 2: mmq_tile<TY, FUSED, 2, XG>(a, smem, tinfo); break;
-    default: mmq_tile<TY, FUSED, 1, XG>(a, smem, tinfo); break;
+    case 2:
+        if (a.wide) mmq_tile<TY, FUSED, 2, XG, 128>(a, smem, tinfo);
+        else mmq_tile<TY, FUSED, 2, XG>(a, smem, tinfo);
+        break;
+    default:
+        if (a.wide) mmq_tile<TY, FUSED, 1, XG, 256>(a, smem, tinfo);
+        else mmq_tile<TY, FUSED, 1, XG>(a, smem, tinfo);
+        break;
     }
 }
 
@@ -873,6 +899,9 @@ __global__ void xg_cvt_k(const float4 *__restrict__ x, half4_t *__restrict__ y, 
 // wx (optional) is the base of the last expert, n_exp - 1, which then need
 // not sit at w + (n_exp - 1) * estride (a shared expert kept apart from the
 // routed arena).
+// Q4MI_MMQ_WIDE=0 keeps 64-value stages for every tile class (A/B timing).
+static const bool g_wide = !(getenv("Q4MI_MMQ_WIDE") && getenv("Q4MI_MMQ_WIDE")[0] == '0');
+
 bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, uint64_t estride,
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
              const int32_t *bounds, uint64_t total_rows, float *dst, uint64_t ld, void *hq,
@@ -915,6 +944,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.tiles = g_tiles;
     a.ntiles = g_ntiles;
     a.mt = mt;
+    a.wide = g_wide ? 1u : 0u;
     a.dst = dst;
     a.ld = ld;
     a.hq = (_Float16 *)hq;
@@ -1211,6 +1241,7 @@ static bool xg_args(uint32_t type, const uint8_t *w, uint64_t astride, uint32_t 
     a.tiles = g_tiles;
     a.ntiles = g_ntiles;
     a.mt = MMQ_MB;
+    a.wide = g_wide ? 1u : 0u;
     return true;
 }
 
