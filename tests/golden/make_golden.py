@@ -72,6 +72,27 @@ def main():
     out.update(win_x=xw, win_ids=wids, win_wts=ww,
                win_y=ref.moe_win(n_embd, n_ff, om.T_IQ3_S, om.T_IQ3_S, E, arena, stride, xw,
                                  wids, ww, np.full(4, 3, np.uint32)))
+    # the other weight formats: dequantized rows (all four) and int8 row
+    # dots (the three with a reference CPU int8 kernel)
+    for ty in (om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S, om.T_Q6_K):
+        rng = np.random.default_rng(500 + ty)
+        K = 1024
+        w = synth.matrix(rng, ty, 6, K)
+        rb = om.row_bytes(ty, K)
+        out["fmt%d_sha" % ty] = sha(w)
+        out["fmt%d_deq" % ty] = np.stack([ref.dequant_row(ty, w[r * rb:(r + 1) * rb], K)
+                                          for r in range(6)])
+        if ty != om.T_Q6_K:
+            xx = rng.standard_normal((3, K)).astype(np.float32)
+            out["fmt%d_x" % ty] = xx
+            out["fmt%d_y" % ty] = ref.dot8_rows(ty, w, 6, K, xx)
+    # the router GEMV (q4_gemv) on F32 and BF16 rows
+    rng = np.random.default_rng(601)
+    wr = (rng.standard_normal((32, 512)) * 0.05).astype(np.float32)
+    xr = rng.standard_normal(512).astype(np.float32)
+    wb = (wr.view(np.uint32) >> 16).astype(np.uint16)
+    out.update(router_w=wr, router_x=xr, router_f32=ref.gemv(0, wr, 32, 512, xr),
+               router_bf16=ref.gemv(30, wb.view(np.uint8), 32, 512, xr))
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, os.path.getsize(path), "bytes")

@@ -57,3 +57,31 @@ def test_moe_golden(oracle):
     yw = oracle.moe_tokens(n_embd, n_ff, om.T_IQ3_S, om.T_IQ3_S, arena, stride, G["win_x"],
                            G["win_ids"], G["win_wts"])
     assert rel_err(yw, G["win_y"]) < 1e-5
+
+
+@pytest.mark.parametrize("ty", [om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S, om.T_Q6_K])
+def test_formats_golden(oracle, ty):
+    """Dequantized rows (bit for bit) and int8 row dots (bit for bit, the
+    three formats with a reference CPU int8 kernel) of the other formats."""
+    rng = np.random.default_rng(500 + ty)
+    K = 1024
+    w = synth.matrix(rng, ty, 6, K)
+    assert np.array_equal(sha(w), G["fmt%d_sha" % ty]), "generator changed"
+    rb = om.row_bytes(ty, K)
+    deq = np.stack([oracle.dequant_row(ty, w[r * rb:(r + 1) * rb], K) for r in range(6)])
+    assert np.array_equal(deq.view(np.uint32), G["fmt%d_deq" % ty].view(np.uint32))
+    if ty != om.T_Q6_K:
+        y = oracle.dot8_rows(ty, w, 6, K, G["fmt%d_x" % ty])
+        assert np.array_equal(y.view(np.uint32), G["fmt%d_y" % ty].view(np.uint32))
+
+
+def test_router_golden(oracle):
+    """The oracle's fixed-order router dot against the reference's q4_gemv
+    (another order): within 1e-5 of each row's sum of |w x|."""
+    w, x = G["router_w"], G["router_x"]
+    scale = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    lg = oracle.router(0, w, 32, 512, x)[0]
+    assert np.all(np.abs(lg - G["router_f32"]) <= 1e-5 * scale)
+    wb = (w.view(np.uint32) >> 16).astype(np.uint16)
+    lb = oracle.router(30, wb.view(np.uint8), 32, 512, x)[0]
+    assert np.all(np.abs(lb - G["router_bf16"]) <= 1e-5 * scale)
