@@ -199,6 +199,17 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
                     uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
                     float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
                     uint32_t ostride, int32_t shared_slot, float *d_sg);
+/* d_y[t] += sigmoid(d_w . d_x[t]) * d_sh[t], t < n_tok: the shared
+ * expert's gate applied to its separately computed output, one launch.
+ * Replaces q4_hip_sgate_axpy (src/q4.h:1129-1131, src/q4_rocm.cu:15775-15800;
+ * src/q4_moe.c:2177).  The dot is q4mi_moe_route's fixed order (so sg has the
+ * same bits as its d_sg).  n % 256 == 0, d_w and d_x 16-byte aligned. */
+bool q4_hip_sgate_axpy(float *d_y, const float *d_sh, const float *d_w, const float *d_x,
+                       uint32_t n, uint32_t n_tok);
+/* *out = sigmoid(a . b) (the one-token sgate scalar).  Replaces
+ * q4_hip_dot_sigmoid (src/q4.h:975-976, src/q4_rocm.cu:4890).  n % 256 == 0,
+ * a and b 16-byte aligned. */
+bool q4_hip_dot_sigmoid(const float *a, const float *b, float *out, uint32_t n);
 /* Stable expert pack per token group: the host order of src/q4_moe.c:
  * 3404-3451 (the reference's GPU assign_pf_k orders by atomic arrival).
  * Replaces q4_hip_assign_pf (src/q4.h:1281-1285, src/q4_rocm.cu:6483-6563). */

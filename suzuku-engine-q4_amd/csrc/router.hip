@@ -111,6 +111,46 @@ __global__ __launch_bounds__(256) void router_gemv_k(const uint8_t *__restrict__
     }
 }
 
+// One wave's dot of w and x (K % 256 == 0) in the router's fixed order;
+// every lane returns the total.
+__device__ inline float wave_dot(const float *__restrict__ w, const float *__restrict__ x,
+                                 uint32_t K, uint32_t lane) {
+    float acc = 0.f;
+    for (uint32_t i = 0; i < K / 256; i++) {
+        const float4 a = ((const float4 *)w)[64 * i + lane];
+        const float4 b = ((const float4 *)x)[64 * i + lane];
+        acc = fmaf(a.x, b.x, acc);
+        acc = fmaf(a.y, b.y, acc);
+        acc = fmaf(a.z, b.z, acc);
+        acc = fmaf(a.w, b.w, acc);
+    }
+    return xor_sum64(acc);
+}
+
+// dy[t][i] += sigmoid(w . x[t]) * sh[t][i]: block (bx, t) recomputes its
+// token's gate with its first wave (the same bits in every block) and adds
+// its 256-value slice.
+__global__ __launch_bounds__(256) void sgate_axpy_k(float *__restrict__ dy,
+                                                    const float *__restrict__ sh,
+                                                    const float *__restrict__ w,
+                                                    const float *__restrict__ x, uint32_t n) {
+    __shared__ float s_sg;
+    const uint32_t t = blockIdx.y;
+    if (threadIdx.x < 64) {
+        const float d = wave_dot(w, x + (size_t)t * n, n, threadIdx.x);
+        if (threadIdx.x == 0) s_sg = 1.f / (1.f + expf(-d));
+    }
+    __syncthreads();
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dy[(size_t)t * n + i] = fmaf(s_sg, sh[(size_t)t * n + i], dy[(size_t)t * n + i]);
+}
+
+__global__ void dot_sigmoid_k(const float *__restrict__ a, const float *__restrict__ b,
+                              float *__restrict__ out, uint32_t n) {
+    const float d = wave_dot(a, b, n, threadIdx.x);
+    if (threadIdx.x == 0) *out = 1.f / (1.f + expf(-d));
+}
+
 }  // namespace q4mi
 
 using namespace q4mi;
@@ -170,6 +210,30 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
     if (!launch_ok("router_gemv_k")) return false;
     return route_list_launch(d_logits, d_ids, d_wts, d_nh, n_tok, n_exp, topk, ostride,
                              shared_slot, d_sgw ? d_sg : nullptr);
+}
+
+/* d_y[t] += sigmoid(d_w . d_x[t]) * d_sh[t] for t < n_tok, in one launch
+ * (see include/q4mi.h). */
+bool q4_hip_sgate_axpy(float *d_y, const float *d_sh, const float *d_w, const float *d_x,
+                       uint32_t n, uint32_t n_tok) {
+    if (!d_y || !d_sh || !d_w || !d_x || !n || !n_tok || n % 256 ||
+        (((uintptr_t)d_w | (uintptr_t)d_x) & 15u)) {
+        set_error("q4_hip_sgate_axpy: bad arguments");
+        return false;
+    }
+    sgate_axpy_k<<<dim3((n + 255) / 256, n_tok), dim3(256), 0, stream()>>>(d_y, d_sh, d_w, d_x,
+                                                                          n);
+    return launch_ok("sgate_axpy_k");
+}
+
+/* *out = sigmoid(a . b), one launch (see include/q4mi.h). */
+bool q4_hip_dot_sigmoid(const float *a, const float *b, float *out, uint32_t n) {
+    if (!a || !b || !out || !n || n % 256 || (((uintptr_t)a | (uintptr_t)b) & 15u)) {
+        set_error("q4_hip_dot_sigmoid: bad arguments");
+        return false;
+    }
+    dot_sigmoid_k<<<dim3(1), dim3(64), 0, stream()>>>(a, b, out, n);
+    return launch_ok("dot_sigmoid_k");
 }
 
 }  // extern "C"

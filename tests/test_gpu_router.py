@@ -146,3 +146,27 @@ def test_routed_layer_with_gated_shared_expert(gpu, oracle, n_tok):
     sw = np.concatenate([ow, osg[:, None]], 1).astype(np.float32)
     yo = oracle.moe_tokens(H, F, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x, sid, sw)
     assert rel_err(host(y), yo) <= TOL
+
+
+def test_sgate_axpy_and_dot_sigmoid(gpu, oracle):
+    """q4_hip_sgate_axpy / q4_hip_dot_sigmoid (the reference's separate gate
+    application): sg equals the oracle's gate (the router's dot order) to
+    1e-6, y += sg * sh."""
+    import torch
+    rng = np.random.default_rng(71)
+    n, T = 2048, 5
+    g = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    sh = rng.standard_normal((T, n)).astype(np.float32)
+    y0 = rng.standard_normal((T, n)).astype(np.float32)
+    y = dev(y0)
+    q4mi.check(gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(dev(sh)), q4mi.ptr(dev(g)),
+                                     q4mi.ptr(dev(x)), n, T), "sgate_axpy")
+    out = zeros(1)
+    q4mi.check(gpu.q4_hip_dot_sigmoid(q4mi.ptr(dev(g)), q4mi.ptr(dev(x[2])), q4mi.ptr(out), n),
+               "dot_sigmoid")
+    _, osg = oracle.router(0, np.zeros((1, n), np.float32), 1, n, x, sgw=g)
+    want = y0 + osg[:, None] * sh
+    assert rel_err(host(y), want) <= 1e-5
+    assert abs(float(host(out)[0]) - osg[2]) <= 1e-6 * abs(osg[2])
+    assert not gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), 1000, 1)
