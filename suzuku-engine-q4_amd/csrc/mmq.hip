@@ -174,13 +174,14 @@ struct RawSpec {
 //           sums times d_x accumulate in `inner`, times d_w once per
 //           superblock), else per 32 or 64 values (d_w folded per group);
 //   kTab    entries of the LDS decode table g16 (IQ3_S: codebook as fp16
-//           magnitudes; IQ2_S: codebook bytes; IQ4_NL: byte -> fp16 values of
-//           its two nibbles; Q2_0: byte -> its four fp16 values c - 1).
+//           magnitudes; IQ2_S: codebook as fp16 magnitudes, two entries of
+//           four per grid point; IQ4_NL: byte -> fp16 values of its two
+//           nibbles; Q2_0: byte -> its four fp16 values c - 1).
 template <uint32_t TY>
 struct MmqFmt {
     static constexpr bool kSuper = TY == Q4MI_T_IQ3_S || TY == Q4MI_T_IQ2_S;
     static constexpr uint32_t kTab = TY == Q4MI_T_IQ3_S    ? 512u
-                                     : TY == Q4MI_T_IQ2_S  ? 1024u
+                                     : TY == Q4MI_T_IQ2_S  ? 2048u
                                      : TY == Q4MI_T_IQ4_NL ? 256u
                                      : TY == Q4MI_T_Q2_0   ? 256u
                                                            : 1u;
@@ -300,36 +301,27 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
         A0 = __builtin_bit_cast(half8_t, make_uint4(t0.x, t0.y, t1.x, t1.y));
         A1 = __builtin_bit_cast(half8_t, make_uint4(t2.x, t2.y, t3.x, t3.y));
     } else if constexpr (TY == Q4MI_T_IQ2_S) {
-        // group j: grid entries l = 0..3 (8 values each), index qs[4j+l] with
-        // 2 bits of qh[j]; A0 = entry kh (multiplier of values 0-15), A1 =
-        // entry 2+kh (values 16-31).  Magnitude bytes become fp16 as
-        // 1024 + b (exponent bits 0x64) minus 1024, exactly.
+        // group j: grid points l = 0..3 (8 values each), index qs[4j+l] with
+        // 2 bits of qh[j]; A0 = point kh (multiplier of values 0-15), A1 =
+        // point 2+kh (values 16-31).  The table holds each point's eight
+        // magnitudes as fp16; the sign masks come from the sign byte.
         const uint32_t qs4 = lds_u16(R + 2 + 4 * j) | (lds_u16(R + 4 + 4 * j) << 16);
         const uint32_t sg4 = lds_u16(R + 34 + 4 * j) | (lds_u16(R + 36 + 4 * j) << 16);
         const uint32_t qh = R[66 + j], sc = R[74 + j];
-        const half2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
-        auto entry = [&](uint32_t l, uint32_t mult, half8_t &A) __attribute__((always_inline)) {
+        auto point = [&](uint32_t l, uint32_t mult, half8_t &A) __attribute__((always_inline)) {
             const uint32_t idx = ((qs4 >> (8 * l)) & 0xffu) | ((qh << (8 - 2 * l)) & 0x300u);
-            const uint2 g = L.g16[idx];
+            const uint2 g0 = L.g16[2 * idx], g1 = L.g16[2 * idx + 1];
             const uint32_t sg = (sg4 >> (8 * l)) & 0xffu;
             const uint2 m0 = L.sm16[sg & 15u], m1 = L.sm16[sg >> 4];
             const half2_t mm = {(_Float16)(float)mult, (_Float16)(float)mult};
-            const uint32_t w[4] = {g.x, g.x, g.y, g.y};
-            const uint32_t sel[2] = {0x04010400u, 0x04030402u};
-            const uint32_t msk[4] = {m0.x, m0.y, m1.x, m1.y};
-            uint32_t o[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                half2_t v = __builtin_bit_cast(half2_t,
-                                               __builtin_amdgcn_perm(0x64646464u, w[k], sel[k & 1]));
-                v = v + off;
-                v = __builtin_bit_cast(half2_t, __builtin_bit_cast(uint32_t, v) ^ msk[k]) * mm;
-                o[k] = __builtin_bit_cast(uint32_t, v);
-            }
-            A = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+            const uint32_t o0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g0.x ^ m0.x) * mm);
+            const uint32_t o1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g0.y ^ m0.y) * mm);
+            const uint32_t o2 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g1.x ^ m1.x) * mm);
+            const uint32_t o3 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g1.y ^ m1.y) * mm);
+            A = __builtin_bit_cast(half8_t, make_uint4(o0, o1, o2, o3));
         };
-        entry(kh, 2u * (sc & 15u) + 1u, A0);
-        entry(2 + kh, 2u * (sc >> 4) + 1u, A1);
+        point(kh, 2u * (sc & 15u) + 1u, A0);
+        point(2 + kh, 2u * (sc >> 4) + 1u, A1);
     } else {
         // Q8_0 block j of the superblock: qs at 34j+2; values 8kh.. and 16+8kh..
         const uint8_t *qs = R + 34 * j + 2;
@@ -542,17 +534,17 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             L.g16[tid + 256 * h2] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }
     }
-    if constexpr (TY == Q4MI_T_IQ2_S) {   // codebook magnitude bytes
+    if constexpr (TY == Q4MI_T_IQ2_S) {   // codebook magnitudes as fp16
         for (uint32_t i = tid; i < 1024; i += 256) {
             const uint32_t c = q4mi_iq2s_code_dev[i];
-            uint32_t lo = 0, hi = 0;
+            uint32_t h[8];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const uint32_t x0 = (c >> (2 * jj)) & 3u, x1 = (c >> (2 * jj + 8)) & 3u;
-                lo |= (x0 == 0 ? 8u : x0 == 1 ? 25u : 43u) << (8 * jj);
-                hi |= (x1 == 0 ? 8u : x1 == 1 ? 25u : 43u) << (8 * jj);
+            for (int jj = 0; jj < 8; jj++) {
+                const uint32_t v = (c >> (2 * jj)) & 3u;
+                h[jj] = __builtin_bit_cast(uint16_t, (_Float16)(v == 0 ? 8.f : v == 1 ? 25.f : 43.f));
             }
-            L.g16[i] = make_uint2(lo, hi);
+            L.g16[2 * i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            L.g16[2 * i + 1] = make_uint2(h[4] | (h[5] << 16), h[6] | (h[7] << 16));
         }
     }
     if constexpr (TY == Q4MI_T_IQ4_NL) {   // byte -> fp16 of both nibbles' values
