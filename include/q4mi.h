@@ -321,8 +321,8 @@ bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type,
  * 128, slot, expert}, weights at abase + slot*astride + og/ou/od, x16 / h16
  * fp16 rows, q4_xg_gu writes h = silu(gate.x)*(up.x) as fp16 [rows][n_ff],
  * q4_xg_dn writes fp32 [rows][n_embd] for the expert reduce.  Types here:
- * IQ3_S and Q8_0 for both (the reference's gate/up IQ2_S / IQ3_XXS / IQ3_S /
- * IQ4_XS, down IQ4_NL / Q2_0).  Numerics are the reference XG's, not the q8
+ * gate/up IQ3_S, Q8_0, IQ2_S; down IQ3_S, Q8_0, IQ4_NL, Q2_0, IQ2_S (the
+ * reference's gate/up IQ2_S / IQ3_XXS / IQ3_S / IQ4_XS, down IQ4_NL / Q2_0).  Numerics are the reference XG's, not the q8
  * path's: this is its A/B. */
 int q4_xg_on(void);
 bool q4_xg_gu_type(uint32_t type);

@@ -629,8 +629,18 @@ void or_xg_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *o);
  * ws = fp16(block scale * 256) (IQ3_S: d * (2s+1); Q8_0: d), the reference
  * XG's dequantization (src/q4_xg.cu:29-35, :60-80). */
 static void or_xg_row(uint32_t type, const uint8_t *w, uint64_t n, float *o) {
-    int32_t wi[32], mult;
+    int32_t wi[32], mult, lm[8];
     for (uint64_t g = 0; g < n / 32; g++) {
+        if (or_other(type)) {   /* IQ4_NL, Q2_0: d; IQ2_S: d/8 times the half's (2s+1) */
+            float d;
+            or_group_other(type, w, g, wi, lm, &d);
+            for (int i = 0; i < 32; i++) {
+                const float ws = or_fp16_round(type == OR_T_IQ2_S ? d * (float)lm[i / 4] * 256.f
+                                                                  : d * 256.f);
+                o[32 * g + i] = or_fp16_round((float)wi[i] * ws);
+            }
+            continue;
+        }
         or_group_ints(type, w, g, wi, &mult);
         uint16_t dh;
         memcpy(&dh, type == OR_T_Q8_0 ? w + 34 * g : w + 110 * (g / 8), 2);

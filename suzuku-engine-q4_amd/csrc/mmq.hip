@@ -291,6 +291,11 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
         }
         A0 = __builtin_bit_cast(half8_t, make_uint4(o0[0], o0[1], o0[2], o0[3]));
         A1 = __builtin_bit_cast(half8_t, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+        if constexpr (XG) {   // times fp16(d * kXgWs), rounded to fp16
+            const _Float16 ws = (_Float16)(q4mi_h2f(lds_u16(R + 18 * j)) * kXgWs);
+            A0 = A0 * ws;
+            A1 = A1 * ws;
+        }
     } else if constexpr (TY == Q4MI_T_Q2_0) {
         // group j = half j&1 of block j>>1; code byte b holds values 4b..4b+3:
         // A0 = bytes 2kh, 2kh+1; A1 = bytes 4+2kh, 5+2kh
@@ -300,6 +305,11 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
         const uint2 t2 = L.g16[b & 0xffu], t3 = L.g16[b >> 8];
         A0 = __builtin_bit_cast(half8_t, make_uint4(t0.x, t0.y, t1.x, t1.y));
         A1 = __builtin_bit_cast(half8_t, make_uint4(t2.x, t2.y, t3.x, t3.y));
+        if constexpr (XG) {   // times fp16(d * kXgWs), rounded to fp16
+            const _Float16 ws = (_Float16)(q4mi_h2f(lds_u16(R + 18 * (j >> 1))) * kXgWs);
+            A0 = A0 * ws;
+            A1 = A1 * ws;
+        }
     } else if constexpr (TY == Q4MI_T_IQ2_S) {
         // group j: grid points l = 0..3 (8 values each), index qs[4j+l] with
         // 2 bits of qh[j]; A0 = point kh (multiplier of values 0-15), A1 =
@@ -313,7 +323,10 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
             const uint2 g0 = L.g16[2 * idx], g1 = L.g16[2 * idx + 1];
             const uint32_t sg = (sg4 >> (8 * l)) & 0xffu;
             const uint2 m0 = L.sm16[sg & 15u], m1 = L.sm16[sg >> 4];
-            const half2_t mm = {(_Float16)(float)mult, (_Float16)(float)mult};
+            // XG: the multiplier becomes fp16(d / 8 * (2s+1) * kXgWs)
+            const float mf = XG ? q4mi_h2f(lds_u16(R)) * 0.125f * (float)mult * kXgWs
+                                : (float)mult;
+            const half2_t mm = {(_Float16)mf, (_Float16)mf};
             const uint32_t o0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g0.x ^ m0.x) * mm);
             const uint32_t o1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g0.y ^ m0.y) * mm);
             const uint32_t o2 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, g1.x ^ m1.x) * mm);
@@ -1164,8 +1177,9 @@ bool q4mi_mmq_gate_up_parts(const void *w_gate, const void *w_up, uint32_t type,
  * q4_xg, src/q4_xg.cu, src/q4.h:1177-1199): weights dequantized to fp16
  * (times 256), activations fp16, fp32 accumulation over the whole K; gate/up
  * writes h = silu(g)*u as fp16 rows, down writes fp32 rows.  Here gate/up
- * IQ3_S or Q8_0 and down IQ3_S or Q8_0 (the reference: gate/up IQ2_S /
- * IQ3_XXS / IQ3_S / IQ4_XS, down IQ4_NL / Q2_0). */
+ * IQ3_S, Q8_0 or IQ2_S and down IQ3_S, Q8_0, IQ4_NL, Q2_0 or IQ2_S (the
+ * reference: gate/up IQ2_S / IQ3_XXS / IQ3_S / IQ4_XS, down IQ4_NL /
+ * Q2_0). */
 int q4_xg_on(void) {
     static int v = -1;
     if (v < 0) {
@@ -1174,8 +1188,13 @@ int q4_xg_on(void) {
     }
     return v;
 }
-bool q4_xg_gu_type(uint32_t t) { return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0; }
-bool q4_xg_dn_type(uint32_t t) { return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0; }
+bool q4_xg_gu_type(uint32_t t) {
+    return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0 || t == Q4MI_T_IQ2_S;
+}
+bool q4_xg_dn_type(uint32_t t) {
+    return t == Q4MI_T_IQ3_S || t == Q4MI_T_Q8_0 || t == Q4MI_T_IQ4_NL || t == Q4MI_T_Q2_0 ||
+           t == Q4MI_T_IQ2_S;
+}
 bool q4_xg_shape_ok(uint32_t n_embd, uint32_t n_ff) {
     return n_embd % MMQ_NB == 0 && n_ff % 64 == 0 && n_embd % 512 == 0 && n_ff % 512 == 0 &&
            n_embd <= 65536 && n_ff <= 65536;
@@ -1257,8 +1276,11 @@ bool q4_xg_gu(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t og
     a.act_row = d_atok;
     a.hq = (_Float16 *)h16;
     const dim3 grid(n_ff / 64, n_tiles);
-    return type == Q4MI_T_IQ3_S ? xg_launch<Q4MI_T_IQ3_S, true>(a, grid)
-                                : xg_launch<Q4MI_T_Q8_0, true>(a, grid);
+    switch (type) {
+    case Q4MI_T_IQ3_S: return xg_launch<Q4MI_T_IQ3_S, true>(a, grid);
+    case Q4MI_T_IQ2_S: return xg_launch<Q4MI_T_IQ2_S, true>(a, grid);
+    default: return xg_launch<Q4MI_T_Q8_0, true>(a, grid);
+    }
 }
 
 /* out[row][n_embd] (fp32) = down . h16[row] over the tiles; expert down
@@ -1279,8 +1301,13 @@ bool q4_xg_dn(uint32_t type, const uint8_t *abase, uint64_t astride, uint64_t od
     a.dst = out;
     a.ld = n_embd;
     const dim3 grid(n_embd / MMQ_NB, n_tiles);
-    return type == Q4MI_T_IQ3_S ? xg_launch<Q4MI_T_IQ3_S, false>(a, grid)
-                                : xg_launch<Q4MI_T_Q8_0, false>(a, grid);
+    switch (type) {
+    case Q4MI_T_IQ3_S: return xg_launch<Q4MI_T_IQ3_S, false>(a, grid);
+    case Q4MI_T_IQ2_S: return xg_launch<Q4MI_T_IQ2_S, false>(a, grid);
+    case Q4MI_T_IQ4_NL: return xg_launch<Q4MI_T_IQ4_NL, false>(a, grid);
+    case Q4MI_T_Q2_0: return xg_launch<Q4MI_T_Q2_0, false>(a, grid);
+    default: return xg_launch<Q4MI_T_Q8_0, false>(a, grid);
+    }
 }
 
 /* h[r][k] = silu(gu[r][k]) * gu[r][n_ff + k]. */

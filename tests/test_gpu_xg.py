@@ -48,13 +48,28 @@ def zeros(shape, dtype=None):
     return torch.zeros(shape, dtype=dtype or torch.float32, device="cuda")
 
 
-@pytest.mark.parametrize("ty", [T_IQ3_S, T_Q8_0])
-def test_xg_layer_matches_oracle(gpu, oracle, ty):
+def packed(rng, E, H, F, tg, td):
+    """Packed experts gate | up | down with gate/up type tg, down type td."""
+    g = synth.matrix(rng, tg, E * F, H)
+    u = synth.matrix(rng, tg, E * F, H)
+    d = synth.matrix(rng, td, E * H, F)
+    gs, ds = F * om.row_bytes(tg, H), H * om.row_bytes(td, F)
+    arena = np.concatenate([np.concatenate([g[e * gs:(e + 1) * gs], u[e * gs:(e + 1) * gs],
+                                            d[e * ds:(e + 1) * ds]]) for e in range(E)])
+    return arena, 2 * gs + ds, 0, gs, 2 * gs
+
+
+@pytest.mark.parametrize("ty,td", [(T_IQ3_S, T_IQ3_S), (T_Q8_0, T_Q8_0), (22, 20), (22, 42),
+                                   (T_IQ3_S, 22)])
+def test_xg_layer_matches_oracle(gpu, oracle, ty, td):
     import torch
     E, H, F, T, k = 48, 2048, 512, 384, 6
-    rng = np.random.default_rng(70 + ty)
-    arena = synth.expert_arena(rng, E, H, F, ty)
-    stride, og, ou, od = synth.expert_stride(H, F, ty)
+    rng = np.random.default_rng(70 + ty + td)
+    if ty == td:
+        arena = synth.expert_arena(rng, E, H, F, ty)
+        stride, og, ou, od = synth.expert_stride(H, F, ty)
+    else:
+        arena, stride, og, ou, od = packed(rng, E, H, F, ty, td)
     x = (rng.standard_normal((T, H)) * 0.05).astype(np.float32)
     lg = synth.logits(rng, T, E, zipf=True)
     ids, wts = oracle.softmax_topk(lg, k)
@@ -64,7 +79,7 @@ def test_xg_layer_matches_oracle(gpu, oracle, ty):
     ek = pk["ek"][:E].astype(np.uint32)
     ebase = pk["bounds"][:E].astype(np.uint32)
     slot = np.arange(E, dtype=np.int32)
-    assert gpu.q4_xg_shape_ok(H, F) and gpu.q4_xg_gu_type(ty) and gpu.q4_xg_dn_type(ty)
+    assert gpu.q4_xg_shape_ok(H, F) and gpu.q4_xg_gu_type(ty) and gpu.q4_xg_dn_type(td)
     cap = gpu.q4_xg_tile_cap(rows, E)
     nt = gpu.q4_xg_tiles(ek.ctypes.data, ebase.ctypes.data, slot.ctypes.data, E,
                          tiles.ctypes.data, cap)
@@ -78,7 +93,7 @@ def test_xg_layer_matches_oracle(gpu, oracle, ty):
     q4mi.check(gpu.q4_xg_cvt(P(dx), P(x16), T * H), "q4_xg_cvt")
     q4mi.check(gpu.q4_xg_gu(ty, P(d_arena), stride, og, ou, H, F, P(d_tiles), nt, P(x16),
                             P(dev(pk["a_tok"][:rows])), P(h16)), "q4_xg_gu")
-    q4mi.check(gpu.q4_xg_dn(ty, P(d_arena), stride, od, F, H, P(d_tiles), nt, P(h16), P(pd)),
+    q4mi.check(gpu.q4_xg_dn(td, P(d_arena), stride, od, F, H, P(d_tiles), nt, P(h16), P(pd)),
                "q4_xg_dn")
     q4mi.check(gpu.q4_hip_expert_reduce(P(y), P(pd), P(dev(pk["rsrc"])), P(dev(pk["rw"])), T, k,
                                         H), "reduce")
@@ -108,7 +123,7 @@ def test_xg_layer_matches_oracle(gpu, oracle, ty):
             nh += F
             nflip += int(np.count_nonzero(~exact))
             # the down launch on the GPU's own h16
-            pdo = oracle.xg_dn_row(F, H, ty, pe[od:], g)
+            pdo = oracle.xg_dn_row(F, H, td, pe[od:], g)
             assert rel_err(pdg[p], pdo) <= 1e-3, (t, j)
             yc[si] = yc[si] + np.float32(wts[t, j]) * pdo
     print("xg h16 values off by one fp16 step: %d of %d" % (nflip, nh))
@@ -117,13 +132,13 @@ def test_xg_layer_matches_oracle(gpu, oracle, ty):
     # of h16 moves y by more than the bar wherever y is small, so the end to
     # end comparison with the oracle's own h16 is reported, not asserted)
     assert rel_err(yg[samp], yc) <= 1e-3
-    yo = oracle.xg_tokens(H, F, ty, ty, arena, stride, x[samp], ids[samp], wts[samp])
+    yo = oracle.xg_tokens(H, F, ty, td, arena, stride, x[samp], ids[samp], wts[samp])
     print("xg layer vs oracle xg layer (own h16 rounding): max rel %.3g, normwise %.3g"
           % (rel_err(yg[samp], yo), np.abs(yg[samp] - yo).max() / np.abs(yo).max()))
     assert np.abs(yg[samp] - yo).max() <= 1e-3 * np.abs(yo).max()
     # the A/B: the q8 path's layer on the same input differs by the q8
     # quantization of x and h (reported, loosely bounded)
-    yq = oracle.moe_tokens(H, F, ty, ty, arena, stride, x[samp], ids[samp], wts[samp], mode=1)
+    yq = oracle.moe_tokens(H, F, ty, td, arena, stride, x[samp], ids[samp], wts[samp], mode=1)
     nw = np.abs(yg[samp] - yq).max() / np.abs(yq).max()
     print("xg vs q8 layer: normwise %.3g" % nw)
     assert nw <= 0.05
@@ -131,5 +146,5 @@ def test_xg_layer_matches_oracle(gpu, oracle, ty):
 
 def test_xg_rejects(gpu):
     assert not gpu.q4_xg_shape_ok(2048, 500)
-    assert not gpu.q4_xg_gu_type(20)
+    assert not gpu.q4_xg_gu_type(20) and not gpu.q4_xg_dn_type(14)
     assert gpu.q4_xg_tiles(None, None, None, 0, None, 0) == 0
