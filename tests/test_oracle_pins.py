@@ -316,7 +316,9 @@ def test_xg_fp16_rounding(oracle):
                                   1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -2049.0, 2051.0])
                         ]).astype(np.float32)
     got = np.array([oracle.L.or_f16_bits(float(f)) for f in v], np.uint16)
-    assert np.array_equal(got, v.astype(np.float16).view(np.uint16))
+    with np.errstate(over="ignore"):     # 65520 and 70000 overflow to inf, as intended
+        want = v.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
 
 
 def test_xg_dequant_close_to_float_dequant(oracle):
