@@ -170,3 +170,50 @@ def test_sgate_axpy_and_dot_sigmoid(gpu, oracle):
     assert rel_err(host(y), want) <= 1e-5
     assert abs(float(host(out)[0]) - osg[2]) <= 1e-6 * abs(osg[2])
     assert not gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), 1000, 1)
+
+
+def test_routed_window_graph_replays(gpu):
+    """Router front + verify window captured once in a HIP graph and
+    replayed over three inputs (new x copied in between, eager work and
+    synchronizations between replays): every replay equals the eager call
+    bit for bit (no memset nodes; deterministic kernels)."""
+    import torch
+    from test_gpu_decode import layer
+    ly = layer()
+    H, F, n_tok = ly.n_embd, ly.n_ff, 4
+    rng = np.random.default_rng(88)
+    w = dev(router_rows(rng, 0, 512, H))
+    g = dev((rng.standard_normal(H) * 0.02).astype(np.float32))
+    xs = [rng.standard_normal((n_tok, H)).astype(np.float32) for _ in range(3)]
+    x = dev(xs[0])
+    lg, ids, wts = zeros((n_tok, 512)), zeros((n_tok, 64), torch.int32), zeros((n_tok, 64))
+    nh, sg, y = zeros(n_tok, torch.int32), zeros(n_tok), zeros((n_tok, H))
+    P = q4mi.ptr
+
+    def layer_call():
+        q4mi.check(gpu.q4mi_moe_route(P(w), 0, P(g), P(x), n_tok, H, 512, 10, P(lg), P(ids),
+                                      P(wts), P(nh), 64, 512, P(sg)), "route")
+        q4mi.check(gpu.q4_hip_moe_exec_win(P(ly.d_arena), ly.stride, P(ids), P(wts), P(nh),
+                                           n_tok, T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od,
+                                           P(x), None, P(y), F, H, H), "exec_win")
+    eager = []
+    for xi in xs:
+        x.copy_(torch.from_numpy(xi).cuda())
+        y.zero_()
+        layer_call()
+        eager.append(host(y).copy())
+    gr = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr, stream=s):
+        q4mi.use_torch_stream()
+        layer_call()
+    q4mi.use_torch_stream()
+    for i, xi in enumerate(xs):
+        x.copy_(torch.from_numpy(xi).cuda())
+        y.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        got = host(y)
+        assert np.array_equal(got.view(np.uint32), eager[i].view(np.uint32)), i
