@@ -320,3 +320,67 @@ def test_shared_expert_in_routed_launch(gpu):
     assert np.array_equal(cx[rows * F:], cs) and np.array_equal(dxs[rows * F // 32:], ds)
     assert np.array_equal(host(pd_x)[:rows], host(pd)) and np.array_equal(host(pd_x)[rows:], host(pd_s))
     assert rel_err(host(y2), host(y1)) <= 1e-5
+
+
+def test_prefill_graph_replays(gpu):
+    """The fused prefill sequence (route, pack, q8(x), gate/up, down, reduce)
+    captured in a HIP graph and replayed over three inputs equals the eager
+    calls bit for bit (no memset nodes; every kernel deterministic)."""
+    import torch
+    E, H, F, T, k = 64, 2048, 512, 256, 6
+    rng = np.random.default_rng(51)
+    arena = synth.expert_arena(rng, E + 1, H, F)
+    stride, og, ou, od = synth.expert_stride(H, F)
+    d_arena = dev(arena)
+    xs = [rng.standard_normal((T, H)).astype(np.float32) for _ in range(3)]
+    lgs = [synth.logits(rng, T, E, zipf=True) for _ in range(3)]
+    x, lg = dev(xs[0]), dev(lgs[0])
+    i32 = torch.int32
+    rows = T * k
+    ids, wts = zeros((T, k), i32), zeros((T, k))
+    a_tok = zeros(rows + T, i32)
+    a_tok[rows:] = torch.arange(T, dtype=i32, device="cuda")
+    rsrc, rw = zeros(rows, i32), zeros(rows)
+    stg, stgn, ek = zeros(512, i32), zeros(1, i32), zeros(512, i32)
+    bounds = zeros(E + 2, i32)
+    bounds[E + 1] = rows + T
+    xq = zeros(int(gpu.q4_mmq_q8_bytes(T, H)), torch.uint8)
+    hq = zeros(int(gpu.q4_mmq_q8_bytes(rows + T, F)), torch.uint8)
+    pd = zeros((rows + T, H))
+    y = zeros((T, H))
+    L, P, chk = gpu, q4mi.ptr, q4mi.check
+    A = d_arena.data_ptr()
+    S = A + E * stride
+
+    def layer():
+        chk(L.q4_hip_route_pf(P(lg), P(ids), P(wts), T, E, k), "route")
+        chk(L.q4mi_assign(P(ids), P(wts), P(a_tok), P(rsrc), P(rw), P(stg), P(stgn), P(ek),
+                          P(bounds), T, k, E, T), "assign")
+        chk(L.q4_mmq_quantize(P(x), None, P(xq), T_IQ3_S, H, T), "q8 x")
+        chk(L.q4mi_mmq_gate_up_x(A, S, T_IQ3_S, F, H, stride, E, P(xq), T, P(a_tok),
+                                 P(bounds), rows + T, P(hq)), "gate/up")
+        chk(L.q4mi_mmq_mul_id_x(A + od, S + od, T_IQ3_S, H, F, stride, E, P(hq), P(bounds),
+                                rows + T, P(pd), H), "down")
+        chk(L.q4mi_expert_reduce_x(P(y), P(pd), P(rsrc), P(rw), T, k, H, rows, None), "reduce")
+    eager = []
+    for xi, li in zip(xs, lgs):
+        x.copy_(torch.from_numpy(xi).cuda())
+        lg.copy_(torch.from_numpy(li).cuda())
+        y.zero_()
+        layer()
+        eager.append(host(y).copy())
+    gr = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr, stream=s):
+        q4mi.use_torch_stream()
+        layer()
+    q4mi.use_torch_stream()
+    for i, (xi, li) in enumerate(zip(xs, lgs)):
+        x.copy_(torch.from_numpy(xi).cuda())
+        lg.copy_(torch.from_numpy(li).cuda())
+        y.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        assert np.array_equal(host(y).view(np.uint32), eager[i].view(np.uint32)), i
