@@ -448,6 +448,43 @@ def bench_floors(M, torch, q4mi, n=48, reps=20):
         del g
     del src
     torch.cuda.empty_cache()
+    # the chip's own floor: plain register-load streaming with many
+    # 256-thread blocks (no LDS, one block per 4096*unroll bytes), same
+    # graph of n back-to-back launches over distinct memory
+    plain = {}
+    for mb in (5, 10, 37):
+        for unroll in (1, 4, 8):
+            per = 4096 * unroll
+            nbytes = (mb * 1000 * 1000 + per - 1) // per * per
+            buf = torch.empty(n * nbytes, dtype=torch.uint8, device="cuda")
+            buf.fill_(1)
+
+            def plaunch():
+                for i in range(n):
+                    q4mi.check(M.q4mi_plain_stream_probe(P(buf) + i * nbytes, nbytes, unroll),
+                               "plain stream probe", M)
+            plaunch()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                q4mi.use_torch_stream(M)
+                plaunch()
+            q4mi.use_torch_stream(M)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / (reps * n)
+            plain["%dMB_unroll%d" % (mb, unroll)] = {
+                "us_per_launch": round(t * 1e6, 2), "blocks": nbytes // per,
+                "GB/s": round(nbytes / t / 1e9, 1)}
+            del g, buf
+            torch.cuda.empty_cache()
+    res["plain_stream"] = plain
     return res
 
 
@@ -749,19 +786,36 @@ def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, label, reps=3
                                    nt), "q4_mmvq_n")
     run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+
+    def clock(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    t_eager = clock(run)
+    # the same calls captured once and replayed: launch-bound host overhead
+    # (a Python call per GEMV) taken out, as a serving loop's graph does
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q4mi.use_torch_stream()
         run()
-    e1.record()
+    q4mi.use_torch_stream()
+    g.replay()
     torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3 / (reps * copies)
+    t = clock(g.replay)
     nbytes = rows * rb + 4 * nt * K + 4 * nt * rows
-    del ws
+    del ws, g
     return {"baseline_config": label, "us": round(t * 1e6, 2),
             "GB/s": round(nbytes / t / 1e9, 1),
             "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
-            "note": "fp32 x in, q8 quantization included (inside the GEMV blocks for <= 1024 row tiles, else one quantize launch); eager launches"}
+            "us_eager": round(t_eager * 1e6, 2),
+            "note": "fp32 x in, q8 quantization included (inside the GEMV blocks for <= 1024 "
+                    "row tiles, else one quantize launch); us = graph replay of the %d "
+                    "back-to-back calls over distinct weight copies, us_eager = the same "
+                    "calls launched eagerly from Python" % copies}
 
 
 if __name__ == "__main__":

@@ -32,6 +32,10 @@ bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops);
  * per_block = 0 launches the same grid empty.  *bytes = the launch's
  * total.  The floors of the decode kernels' structure. */
 bool q4mi_stream_probe(const void *src, uint32_t per_block, uint32_t waves, uint64_t *bytes);
+/* One launch of the plain streaming probe, the chip's own floor: `bytes`
+ * (a multiple of 4096 * unroll) read from src by 256-thread blocks with
+ * `unroll` (1, 4 or 8) 16-byte register loads per thread, nothing written. */
+bool q4mi_plain_stream_probe(const void *src, uint64_t bytes, uint32_t unroll);
 
 #ifdef __cplusplus
 }

@@ -229,7 +229,17 @@ struct MmqArgs {
     _Float16 *hq;           // fused mode: [rows][n_ff] fp16 codes of h
     float *hd;              // fused mode: [rows][n_ff/32]
     uint32_t wide;          // one- and two-sub-tile tiles use 256 / 128-value stages
+    uint32_t ko;            // measurement build: knockout bits (timing studies only)
 };
+
+// Knockouts of a timing-study build (-DQ4MI_MMQ_KO=bits):
+// parts of the tile loop switched off to time what each costs.  Results are
+// garbage with any bit set; the product library compiles them out.
+#ifdef Q4MI_MMQ_KO
+#define MMQ_KO(a, bit) (((Q4MI_MMQ_KO) >> (bit)) & 1u)
+#else
+#define MMQ_KO(a, bit) false
+#endif
 
 __device__ inline uint32_t lds_u16(const uint8_t *p) { return *(const uint16_t *)p; }
 
@@ -247,12 +257,19 @@ template <uint32_t TY, bool XG = false>
 __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t j,
                                 uint32_t kh, half8_t &A0, half8_t &A1) {
     if constexpr (TY == Q4MI_T_IQ3_S) {
+#if defined(Q4MI_MMQ_KO) && ((Q4MI_MMQ_KO >> 9) & 1)
+        const uint32_t lv = (uint32_t)(uintptr_t)R;
+        const uint32_t qa = (lv * 7u + j) & 0xffffu, qb = (lv * 13u + j) & 0xffffu;
+        const uint32_t qh = (lv >> 3) & 0xffu, sa = (lv >> 5) & 0xffu, sb = (lv >> 7) & 0xffu;
+        const uint32_t sc = (lv >> 2) & 0xffu;
+#else
         const uint32_t qa = lds_u16(R + 2 + 8 * j + 2 * kh);       // qs entries 2kh, 2kh+1
         const uint32_t qb = lds_u16(R + 2 + 8 * j + 4 + 2 * kh);   // 4+2kh, 5+2kh
         const uint32_t qh = R[66 + j];
         const uint32_t sa = R[74 + 4 * j + kh];                    // sign nibbles 2kh, 2kh+1
         const uint32_t sb = R[74 + 4 * j + 2 + kh];                // 4+2kh, 5+2kh
         const uint32_t sc = R[106 + (j >> 1)];
+#endif
         float m = (float)(2u * ((j & 1u) ? (sc >> 4) : (sc & 15u)) + 1u);
         if constexpr (XG) m = q4mi_h2f(lds_u16(R)) * m * kXgWs;
         const half2_t mm = {(_Float16)m, (_Float16)m};
@@ -263,8 +280,13 @@ __device__ inline void decode_a(const MmqLds<TY> &L, const uint8_t *R, uint32_t 
             const uint32_t qs8 = ((q < 2 ? qa : qb) >> (8 * (q & 1))) & 0xffu;
             const uint32_t idx = qs8 | (((qh >> e) & 1u) << 8);
             const uint32_t nib = ((q < 2 ? sa : sb) >> (4 * (q & 1))) & 15u;
+#if defined(Q4MI_MMQ_KO) && ((Q4MI_MMQ_KO >> 8) & 1)
+            const uint2 g = make_uint2(idx * 0x00010001u, idx * 0x00030001u);
+            const uint2 s = make_uint2(nib << 15, nib << 31);
+#else
             const uint2 g = L.g16[idx];
             const uint2 s = L.sm16[nib];
+#endif
             half2_t a = __builtin_bit_cast(half2_t, g.x ^ s.x) * mm;
             half2_t b = __builtin_bit_cast(half2_t, g.y ^ s.y) * mm;
             o[2 * q] = __builtin_bit_cast(uint32_t, a);
@@ -600,23 +622,32 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         // (one stage per superblock: its raw bytes land only with this
         // stage's wait, so the decode follows the barriers)
         const bool ahead = SPS >= 2 && s != 0;
-        if (ahead) decode();
+        if (ahead && !MMQ_KO(a, 2)) decode();
         // every wave is done with stage s-1 (and at a superblock start with
         // superblock sbi-1): their buffers may be refilled.  The reads in
         // flight here are the decode's, of a buffer nobody refills now.
-        mmq_bar_rd();
+        if (!MMQ_KO(a, 0)) mmq_bar_rd();
         // issue the next copies, then wait for this wave's part of stage s
         // (the copies just issued stay in flight)
         const bool nraw = q == 0 && sbi + 1 < nsb, nstage = s + 1 < nst;
-        if (nraw) issue_raw(sbi + 1);
-        if (nstage) issue_stage(s + 1);
-        if (nraw && nstage) mmq_wait<RAW_PER_WAVE + ST_OPS>();
+        if (!MMQ_KO(a, 5)) {
+            if (nraw && !MMQ_KO(a, 6)) issue_raw(sbi + 1);
+            if (nstage && !MMQ_KO(a, 7)) issue_stage(s + 1);
+        }
+        if (MMQ_KO(a, 1) || MMQ_KO(a, 5)) {
+        } else if (nraw && nstage) mmq_wait<RAW_PER_WAVE + ST_OPS>();
         else if (nstage) mmq_wait<ST_OPS>();
         else if (nraw) mmq_wait<RAW_PER_WAVE>();
         else mmq_wait<0>();
-        mmq_bar();                                    // everyone's part is
+        if (!MMQ_KO(a, 0)) mmq_bar();                 // everyone's part is
         const uint32_t buf = s & 1u;
-        if (!ahead) decode();
+        if (MMQ_KO(a, 2)) {
+#pragma unroll
+            for (uint32_t gl = 0; gl < GPS; gl++) {
+                A[gl][0] = half8_t{} + (_Float16)(float)(lane + gl);
+                A[gl][1] = half8_t{} + (_Float16)(float)(lane + 3 * gl);
+            }
+        } else if (!ahead) decode();
         // The stage's 2*NSUB products n = (group gl, token sub-tile t): an
         // exact-integer MFMA pair, then one scale FMA per output.  Product
         // n+1's pair is issued before product n's FMAs, so the FMAs never
@@ -626,17 +657,31 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
             const int gl = n / NSUB, t = n % NSUB;
             const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
             const uint32_t tok = 32 * t + (lane & 31u);
-            const half8_t B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
-            const half8_t B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
-            dxo = dxb[buf * kDxBuf + tok * GPS + gl];
+            half8_t B0, B1;
+            if (MMQ_KO(a, 3)) {
+                B0 = half8_t{} + (_Float16)(float)(tok + gl);
+                B1 = half8_t{} + (_Float16)(float)(tok + t);
+                dxo = (float)n;
+            } else {
+                B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
+                B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
+                dxo = dxb[buf * kDxBuf + tok * GPS + gl];
+            }
             f32x16_t r = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, f32x16_t{}, 0, 0, 0);
             return __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, r, 0, 0, 0);
         };
         auto scale = [&](int n, const f32x16_t &sacc, float dxv) __attribute__((always_inline)) {
             const int gl = n / NSUB, t = n % NSUB;
             if constexpr (MmqFmt<TY>::kSuper) {
+                if (MMQ_KO(a, 4)) {   // one FMA instead of sixteen
+                    float z = sacc[0];
 #pragma unroll
-                for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
+                    for (int i = 1; i < 16; i++) z = fmaxf(z, sacc[i]);
+                    inner[t][n & 15] = fmaf(z, dxv, inner[t][n & 15]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);
+                }
             } else {
                 const uint32_t j = GPS * q + gl;
 #pragma unroll
@@ -692,6 +737,16 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         for (int t = 0; t < NSUB; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[t][i] *= 1.f / kXgWs;   // exact (power of 2)
+    }
+    if (MMQ_KO(a, 10)) {   // no epilogue: one guarded store keeps the results live
+        float z = 0.f;
+#pragma unroll
+        for (int t = 0; t < NSUB; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) z += acc[t][i];
+        float *o = FUSED ? a.hd : a.dst;
+        if (z == 1234.5f) o[tid] = z;
+        return;
     }
     if (!FUSED) {
         // lane: token column 32t + lane%32, weight rows 32wv + 8b + 4kh + 0..3
@@ -950,6 +1005,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.ntiles = g_ntiles;
     a.mt = mt;
     a.wide = g_wide ? 1u : 0u;
+    a.ko = 0;
     a.dst = dst;
     a.ld = ld;
     a.hq = (_Float16 *)hq;

@@ -30,27 +30,61 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nr = min(R, rows - r0);
     const uint32_t G = K / 32;
-    F::init(tab, tid, 256);
-    stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
+    const uint8_t *wsrc = W + (size_t)r0 * rb;
+    // A 16-byte-aligned tile goes out first, all of it from wave 0 (global ->
+    // LDS copies, no registers), so the weight stream starts at once; waves
+    // 1-3 meanwhile build the tables and quantize x.  The VMEM wait count is
+    // per wave, so their own loads' waits never cover the tile copies.  An
+    // unaligned tile is copied through registers by every thread.
+    const bool dma = ((((uintptr_t)wsrc) | (nr * rb)) & 15u) == 0;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (dma) {
+        if (wv == 0) stage_tile_issue(tile, wsrc, nr * rb, tid, 64);
+    } else {
+        stage_tile_issue(tile, wsrc, nr * rb, tid, 256);
+    }
+    // helper threads of the prologue: waves 1-3 (all 256 without a DMA tile)
+    const uint32_t h0 = dma ? 64u : 0u, hid = tid - h0, nh = 256u - h0;
+    if (tid >= h0) F::init(tab, hid, nh);
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
     // pre-quantized codes: loaded while the tile copy is in flight
     if (!xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
-    if (xf) {
-        // 8 lanes per 32-value group, 32 groups per pass
+    if (xf && tid >= h0) {
+        // 8 lanes per 32-value group, nh / 8 groups per pass; the loads of
+        // up to 8 passes are issued before any is used (a load issued
+        // behind the tile copies returns only when they have landed, so one
+        // wait must cover all of them)
         int8_t *lq = (int8_t *)(tile + ((R * rb + 15u) & ~15u));
         float *ld = (float *)(lq + (size_t)NT * K);
-        for (uint32_t gid = tid >> 3; gid < nt * G; gid += 32) {
-            const uint32_t t = gid / G, g = gid % G, sub = tid & 7u;
-            const float4 v = *(const float4 *)(xf + (size_t)t * K + 32u * g + 4u * sub);
-            float dd;
-            int bsum;
-            const uint32_t packed = q4mi_quant_team8(v, &dd, &bsum);
-            *(uint32_t *)(lq + (size_t)t * K + 32u * g + 4u * sub) = packed;
-            if (sub == 0) ld[gid] = dd;
+        const uint32_t ng = nt * G, step = nh / 8, sub = hid & 7u;
+        for (uint32_t g0 = hid >> 3; g0 < ng; g0 += 8 * step) {
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t gid = g0 + k * step;
+                if (gid < ng) {
+                    const uint32_t t = gid / G, g = gid % G;
+                    v[k] = *(const float4 *)(xf + (size_t)t * K + 32u * g + 4u * sub);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t gid = g0 + k * step;
+                if (gid < ng) {   // uniform per 8-lane team
+                    const uint32_t t = gid / G, g = gid % G;
+                    float dd;
+                    int bsum;
+                    const uint32_t packed = q4mi_quant_team8(v[k], &dd, &bsum);
+                    *(uint32_t *)(lq + (size_t)t * K + 32u * g + 4u * sub) = packed;
+                    if (sub == 0) ld[gid] = dd;
+                }
+            }
         }
-        xq = lq;
-        xd = ld;
+    }
+    if (xf) {
+        xq = (const int8_t *)(tile + ((R * rb + 15u) & ~15u));
+        xd = (const float *)(xq + (size_t)NT * K);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();

@@ -63,7 +63,7 @@ constexpr uint32_t kProd = Q4MI_PROD;   // producer waves (issue the LDS copies)
 constexpr uint32_t kCons = kT - kProd * 64;   // consumer threads
 constexpr uint32_t kConsW = kCons / 64;       // consumer waves
 constexpr uint32_t kDnRows = 8;   // output rows per down block
-constexpr uint32_t kMaxS = 16;    // LDS ring slots
+constexpr uint32_t kMaxS = 32;    // LDS ring slots
 struct HostList {
     int32_t id[kMaxU];
     float w[kMaxU];
@@ -544,6 +544,9 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
 #ifdef Q4MI_TRACE
     uint32_t npub = 0, nloop = 0;
 #endif
+#ifdef Q4MI_TRACE
+    Q4MI_TR(17, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
+#endif
     while (pub < C && idle < kSpinMax) {
         while (next < C && (next < pub + kProd * ahead) && slot_free(next)) {
             if (next >= S) lds_st(&y->cons[next % S], 0);
@@ -642,6 +645,13 @@ __device__ inline void gu_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
             const int32_t id = __builtin_amdgcn_readlane(idv, u);
             const uint8_t *e = base + (uint64_t)id * stride + (uint64_t)r * rb;
             issued += dma1<UNIT>(sg + (size_t)(q - q0) * rb, e + og, n * rb, lane);
+#ifdef Q4MI_TRACE
+            if (c == 0 && q == q0) {
+                unsigned long long *const q4tr = a.trace;
+                const uint32_t q4bid = blockIdx.x;
+                Q4MI_TR(18, 0, wave == 0 && lane == 0);
+            }
+#endif
             issued += dma1<UNIT>(su + (size_t)(q - q0) * rb, e + ou, n * rb, lane);
             q += n;
         }
@@ -867,6 +877,13 @@ __device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
             const int32_t id = __builtin_amdgcn_readlane(idv, u);
             const uint8_t *e = base + (uint64_t)id * stride + od + (uint64_t)r0 * rb;
             issued += dma1<UNIT>(dst + (size_t)(u - e0) * nr * rb, e, nr * rb, lane);
+#ifdef Q4MI_TRACE
+            if (c == 0 && u == e0) {
+                unsigned long long *const q4tr = a.trace;
+                const uint32_t q4bid = blockIdx.x;
+                Q4MI_TR(18, 1, wave == 0 && lane == 0);
+            }
+#endif
         }
     };
     auto items = [&](uint32_t c) { return min(ch, nu - c * ch) * nr; };
@@ -1124,6 +1141,9 @@ static size_t gu_plan(const MoeArgs &a, uint32_t nu_host, uint32_t grid, size_t 
     const uint32_t pairs = nu_host ? nu_host * a.n_ff : kMaxU * a.n_ff;
     const uint32_t share = (pairs + grid - 1) / grid;
     ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : 8;
+#ifdef Q4MI_TRACE
+    if (getenv("Q4MI_CHUNK")) ch = std::max(1, atoi(getenv("Q4MI_CHUNK")));
+#endif
     const size_t fixed = head_bytes(ty) + al16((size_t)NT * a.K + (size_t)NT * (a.K / 32) * 4);
     S = 0;
     // A consumer wave waits for every chunk its two pairs touch (at most
@@ -1149,6 +1169,9 @@ static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &
                          al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
     const uint32_t nu_est = nu_host ? nu_host : kMaxU;
     ch = std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd);
+#ifdef Q4MI_TRACE
+    if (getenv("Q4MI_DNCHUNK")) ch = std::max(1, atoi(getenv("Q4MI_DNCHUNK")));
+#endif
     S = 0;
     for (;; ch = (ch + 1) / 2) {
         const size_t slot = (size_t)ch * kDnRows * a.rb_dn;

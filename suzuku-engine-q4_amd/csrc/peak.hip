@@ -86,6 +86,26 @@ __global__ __launch_bounds__(1024) void stream_probe_k(const uint8_t *__restrict
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Floor probe of the chip itself (not of the decode kernels' structure):
+// a plain register-load streaming kernel.  Many 256-thread blocks; thread t
+// of block b loads U 16-byte units at src + 16 (b*256*U + u*256 + t), u < U
+// (one coalesced 4 KB wave-group access per u), all issued before any is
+// used.  The loaded words are folded into one value that is stored only if
+// it equals a key the data never produces, so no load can be dropped and
+// nothing is written.
+template <int U>
+__global__ __launch_bounds__(256) void plain_stream_k(const uint4 *__restrict__ src, uint32_t key,
+                                                      uint32_t *__restrict__ sink) {
+    const uint4 *s = src + (size_t)blockIdx.x * 256u * U + threadIdx.x;
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = s[256 * u];
+    uint32_t f = 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) f ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (f == key) sink[threadIdx.x] = f;
+}
+
 }  // namespace q4mi
 
 using namespace q4mi;
@@ -121,6 +141,34 @@ bool q4mi_stream_probe(const void *src, uint32_t per_block, uint32_t waves, uint
     stream_probe_k<<<dim3(blocks), dim3(1024), 150 * 1024, stream()>>>((const uint8_t *)src,
                                                                        per_block, waves);
     return launch_ok("stream_probe_k");
+}
+
+/* Measurement hook: one launch of the plain streaming probe, reading
+ * `bytes` (a multiple of 4096 * unroll) from src with `unroll` (1, 4 or 8)
+ * 16-byte loads per thread in 256-thread blocks.  The probe writes nothing
+ * unless the data XOR-folds to 0x9e3779b9 in some thread (the caller's fill
+ * must avoid that; a uniform byte fill folds to 0). */
+bool q4mi_plain_stream_probe(const void *src, uint64_t bytes, uint32_t unroll) {
+    const uint64_t per = 4096ull * unroll;
+    if (!src || ((uintptr_t)src & 15) || (unroll != 1 && unroll != 4 && unroll != 8) ||
+        !bytes || bytes % per || bytes / per > 0x7fffffffull) {
+        set_error("q4mi_plain_stream_probe: bad arguments");
+        return false;
+    }
+    if (!g_sink) {
+        if (hipMalloc(&g_sink, 1024 * sizeof(float)) != hipSuccess) {
+            set_error("q4mi_plain_stream_probe: sink allocation failed");
+            return false;
+        }
+        g_sink_n = 1024;
+    }
+    const dim3 grid((uint32_t)(bytes / per));
+    uint32_t *sk = (uint32_t *)g_sink;
+    const uint4 *s = (const uint4 *)src;
+    if (unroll == 1) plain_stream_k<1><<<grid, dim3(256), 0, stream()>>>(s, 0x9e3779b9u, sk);
+    else if (unroll == 4) plain_stream_k<4><<<grid, dim3(256), 0, stream()>>>(s, 0x9e3779b9u, sk);
+    else plain_stream_k<8><<<grid, dim3(256), 0, stream()>>>(s, 0x9e3779b9u, sk);
+    return launch_ok("plain_stream_k");
 }
 
 bool q4mi_mfma_probe(int kind, uint32_t iters, uint64_t *ops) {

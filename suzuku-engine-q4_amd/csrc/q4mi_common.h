@@ -106,12 +106,20 @@ __device__ inline uint32_t q4mi_expand4(uint32_t n) {
 __constant__ uint16_t q4mi_iq3s_code_dev[512] = {Q4MI_IQ3S_CODES};
 
 __device__ inline void q4mi_iq3s_tables_init(Iq3sLds *t, int tid, int nthreads) {
-    for (int i = tid; i < 512; i += nthreads) {
-        const uint32_t c = q4mi_iq3s_code_dev[i];
-        uint32_t v = 0;
+    // the codebook loads of four entries go out before any is used
+    for (int i0 = tid; i0 < 512; i0 += 4 * nthreads) {
+        uint32_t c[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) v |= (2u * ((c >> (3 * j)) & 7u) + 1u) << (8 * j);
-        t->grid[i] = v;
+        for (int k = 0; k < 4; k++) c[k] = i0 + k * nthreads < 512 ? q4mi_iq3s_code_dev[i0 + k * nthreads] : 0u;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = i0 + k * nthreads;
+            if (i >= 512) break;
+            uint32_t v = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v |= (2u * ((c[k] >> (3 * j)) & 7u) + 1u) << (8 * j);
+            t->grid[i] = v;
+        }
     }
     for (int i = tid; i < 256; i += nthreads)
         t->smask[i] = make_uint2(q4mi_expand4(i & 15u), q4mi_expand4(i >> 4));
