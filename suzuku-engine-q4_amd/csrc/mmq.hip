@@ -230,6 +230,7 @@ struct MmqArgs {
     float *hd;              // fused mode: [rows][n_ff/32]
     uint32_t wide;          // one- and two-sub-tile tiles use 256 / 128-value stages
     uint32_t ko;            // measurement build: knockout bits (timing studies only)
+    uint32_t xcd;           // XCD-grouped block order (grid rows a multiple of 8)
 };
 
 // Knockouts of a timing-study build (-DQ4MI_MMQ_KO=bits):
@@ -425,7 +426,7 @@ __device__ inline void mmq_bar_rd() { asm volatile("s_barrier" ::: "memory"); }
 // / 2x less often.
 template <uint32_t TY, bool FUSED, int NSUB, bool XG = false, uint32_t KS = 64>
 __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, uint8_t *smem,
-                                                               const int4 tinfo) {
+                                                               const int4 tinfo, uint32_t cblk) {
     MmqLds<TY> &L = *(MmqLds<TY> *)smem;
     constexpr uint32_t SB = RawSpec<TY>::SB;
     constexpr uint32_t SSD = RawSpec<TY>::SS / 4;             // raw slot dwords
@@ -455,7 +456,7 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
     // expert; another tensor in the GGUF layout)
     const uint8_t *Wu = isx ? a.wx_up : We + a.up_off;
     // weight row (within the gate or up matrix) of tile row r
-    const uint32_t nblk = FUSED ? blockIdx.x * 64 : blockIdx.x * MMQ_NB;
+    const uint32_t nblk = FUSED ? cblk * 64 : cblk * MMQ_NB;
     auto wsrc = [&](uint32_t r, uint32_t sbi) -> const uint8_t * {
         const uint8_t *m = (FUSED && r >= 64) ? Wu : We;
         const uint32_t wr = (FUSED && r >= 64) ? nblk + (r - 64) : nblk + r;
@@ -845,24 +846,42 @@ __global__ __launch_bounds__(256) void swiglu_k(const float *__restrict__ gu,
     h[i] = g / (1.f + expf(-g)) * u;
 }
 
+// Block order: the hardware hands workgroups to the 8 XCDs round-robin in
+// linear order (x fastest), so with the plain (column block, tile) grid every
+// XCD's L2 would fetch every tile's activation rows.  With a.xcd set, linear
+// block L runs tile 8 (k / gx) + L % 8 and column block k % gx, k = L / 8:
+// all column blocks of a tile run on one XCD and share its activation rows in
+// that L2 (and consecutive tiles, largest first, go to different XCDs).
+struct MmqBlock {
+    uint32_t col, tile;
+};
+__device__ inline MmqBlock mmq_block(const MmqArgs &a) {
+    if (!a.xcd) return MmqBlock{blockIdx.x, blockIdx.y};
+    const uint32_t gx = gridDim.x;
+    const uint32_t L = blockIdx.x + gx * blockIdx.y, k = L >> 3;
+    return MmqBlock{k % gx, 8u * (k / gx) + (L & 7u)};
+}
+
 template <uint32_t TY, bool FUSED, bool XG = false>
 __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t ti = blockIdx.y;
+    const MmqBlock mb = mmq_block(a);
+    const uint32_t ti = mb.tile;
     const int4 tinfo = a.tiles[ti];          // in bounds: the grid is the list's capacity
     if (ti >= *a.ntiles) return;
+    const uint32_t col = mb.col;
     const int32_t rows = tinfo.z;
     // block-uniform choice of the (branch-free) sub-tile count
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
-    case 4: mmq_tile<TY, FUSED, 4, XG>(a, smem, tinfo); break;
-    case 3: mmq_tile<TY, FUSED, 3, XG>(a, smem, tinfo); break;
+    case 4: mmq_tile<TY, FUSED, 4, XG>(a, smem, tinfo, col); break;
+    case 3: mmq_tile<TY, FUSED, 3, XG>(a, smem, tinfo, col); break;
     case 2:
-        if (a.wide) mmq_tile<TY, FUSED, 2, XG, 128>(a, smem, tinfo);
-        else mmq_tile<TY, FUSED, 2, XG>(a, smem, tinfo);
+        if (a.wide) mmq_tile<TY, FUSED, 2, XG, 128>(a, smem, tinfo, col);
+        else mmq_tile<TY, FUSED, 2, XG>(a, smem, tinfo, col);
         break;
     default:
-        if (a.wide) mmq_tile<TY, FUSED, 1, XG, 256>(a, smem, tinfo);
-        else mmq_tile<TY, FUSED, 1, XG>(a, smem, tinfo);
+        if (a.wide) mmq_tile<TY, FUSED, 1, XG, 256>(a, smem, tinfo, col);
+        else mmq_tile<TY, FUSED, 1, XG>(a, smem, tinfo, col);
         break;
     }
 }
@@ -961,6 +980,8 @@ __global__ void xg_cvt_k(const float4 *__restrict__ x, half4_t *__restrict__ y, 
 // routed arena).
 // Q4MI_MMQ_WIDE=0 keeps 64-value stages for every tile class (A/B timing).
 static const bool g_wide = !(getenv("Q4MI_MMQ_WIDE") && getenv("Q4MI_MMQ_WIDE")[0] == '0');
+// XCD-grouped block order (Q4MI_MMQ_XCD=0 restores the plain order for A/B timing).
+static const bool g_mmq_xcd = !(getenv("Q4MI_MMQ_XCD") && getenv("Q4MI_MMQ_XCD")[0] == '0');
 
 bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, uint64_t estride,
              uint32_t n_exp, const void *xq, uint64_t xrows, const int32_t *act_row,
@@ -975,7 +996,8 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     const uint64_t colblocks = hq ? w_rows / 2 / 64 : w_rows / MMQ_NB;
     uint32_t mt = MT;
     while (mt > 32 && colblocks * ((total_rows + mt - 1) / mt) < 2ull * (uint64_t)cu_count()) mt /= 2;
-    const uint32_t max_tiles = (uint32_t)(total_rows / mt + n_exp + 1);
+    // (a multiple of 8: the XCD-grouped block order maps whole octets)
+    const uint32_t max_tiles = (uint32_t)((total_rows / mt + n_exp + 1 + 7) & ~(uint64_t)7);
     if (max_tiles > 65535) {
         set_error("mmq: too many row tiles (%u)", max_tiles);
         return false;
@@ -1006,6 +1028,7 @@ bool mmq_run(const uint8_t *w, uint32_t ty, uint64_t w_rows, uint64_t w_cols, ui
     a.mt = mt;
     a.wide = g_wide ? 1u : 0u;
     a.ko = 0;
+    a.xcd = g_mmq_xcd ? 1u : 0u;
     a.dst = dst;
     a.ld = ld;
     a.hq = (_Float16 *)hq;
