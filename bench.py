@@ -382,6 +382,7 @@ def main():
         out["decode_floors"] = bench_floors(M, torch, q4mi)
     if not args.no_prefill:
         out["mfma_peak"] = bench_mfma_peak(M, torch, q4mi)
+        out["mmq_inner_ab"] = bench_mmq_ab(M, torch, q4mi)
         out["prefill"] = bench_prefill(L, torch, np, q4mi, synth, args)
         out["prefill"]["pct_of_measured_int8_peak"] = round(
             100 * out["prefill"]["mmq_TOPS"] / out["mfma_peak"]["int8_TOPS"], 2)
@@ -508,6 +509,33 @@ def bench_mfma_peak(L, torch, q4mi, iters=16384, reps=5):
         res[key] = round(ops.value / t / 1e12, 1)
     res["datasheet_int8_TOPS"] = 5000.0
     res["datasheet_fp16_TFLOPS"] = 2500.0
+    return res
+
+
+def bench_mmq_ab(M, torch, q4mi, groups=2048, reps=5):
+    """The prefill MMQ inner loop on the same work, two ways (measurement
+    build's probe): exact-integer fp16 MFMA (this library's design: the IQ3_S
+    multiplier folded into fp16 operands, one scale FMA per output and group)
+    against int8 MFMA (the multiplier does not fit int8, so each output takes
+    an integer multiply, a conversion and an FMA per group).  Rates are the
+    GEMM ops the loop performs, timed with events on the library stream."""
+    import ctypes
+    res = {}
+    for kind, key in ((0, "fp16_exact_TOPS"), (1, "int8_TOPS")):
+        ops = ctypes.c_uint64(0)
+        q4mi.check(M.q4mi_mmq_ab_probe(kind, groups, ctypes.byref(ops)), "mmq A/B probe", M)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            q4mi.check(M.q4mi_mmq_ab_probe(kind, groups, ctypes.byref(ops)), "mmq A/B probe", M)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        res[key] = round(ops.value / t / 1e12, 1)
+    res["int8_over_fp16"] = round(res["int8_TOPS"] / res["fp16_exact_TOPS"], 3)
+    res["note"] = ("inner loop only (operands in LDS, 32 x 128 outputs per wave, 2 blocks per "
+                   "CU): IQ3_S decode + MFMA + per-group scaling, no copies or epilogue")
     return res
 
 

@@ -36,6 +36,12 @@ bool q4mi_stream_probe(const void *src, uint32_t per_block, uint32_t waves, uint
  * (a multiple of 4096 * unroll) read from src by 256-thread blocks with
  * `unroll` (1, 4 or 8) 16-byte register loads per thread, nothing written. */
 bool q4mi_plain_stream_probe(const void *src, uint64_t bytes, uint32_t unroll);
+/* One launch of the prefill MMQ inner-loop A/B (kind 0: exact-integer fp16
+ * MFMA, this library's design; 1: int8 MFMA with the per-row (2s+1)
+ * multiplier and d_x applied per output), 2 blocks per CU, each wave 32 x
+ * 128 outputs over `groups` (a multiple of 8) 32-value groups, operands in
+ * LDS; *ops = the launch's integer ops, for a caller-timed rate. */
+bool q4mi_mmq_ab_probe(int kind, uint32_t groups, uint64_t *ops);
 
 #ifdef __cplusplus
 }

@@ -30,27 +30,19 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nr = min(R, rows - r0);
     const uint32_t G = K / 32;
-    const uint8_t *wsrc = W + (size_t)r0 * rb;
-    // A 16-byte-aligned tile goes out first, all of it from wave 0 (global ->
-    // LDS copies, no registers), so the weight stream starts at once; waves
-    // 1-3 meanwhile build the tables and quantize x.  The VMEM wait count is
-    // per wave, so their own loads' waits never cover the tile copies.  An
-    // unaligned tile is copied through registers by every thread.
-    const bool dma = ((((uintptr_t)wsrc) | (nr * rb)) & 15u) == 0;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (dma) {
-        if (wv == 0) stage_tile_issue(tile, wsrc, nr * rb, tid, 64);
-    } else {
-        stage_tile_issue(tile, wsrc, nr * rb, tid, 256);
-    }
-    // helper threads of the prologue: waves 1-3 (all 256 without a DMA tile)
-    const uint32_t h0 = dma ? 64u : 0u, hid = tid - h0, nh = 256u - h0;
-    if (tid >= h0) F::init(tab, hid, nh);
+    // Tables first, then the tile's copies, then the x loads: a wave's VMEM
+    // operations complete in issue order, so loads issued behind the copies
+    // return when the copies have landed (measured: copies first, or copies
+    // from fewer waves while the others build the table and quantize, are
+    // slower for configs[0]).
+    F::init(tab, tid, 256);
+    stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
+    const uint32_t hid = tid, nh = 256u;
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
     // pre-quantized codes: loaded while the tile copy is in flight
     if (!xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
-    if (xf && tid >= h0) {
+    if (xf) {
         // 8 lanes per 32-value group, nh / 8 groups per pass; the loads of
         // up to 8 passes are issued before any is used (a load issued
         // behind the tile copies returns only when they have landed, so one

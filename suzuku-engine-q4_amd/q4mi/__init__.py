@@ -119,6 +119,7 @@ _MEAS_SIGS = {
     "q4mi_mfma_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
     "q4mi_stream_probe": (_c.c_bool, [_vp, _u32, _u32, _c.POINTER(_c.c_uint64)]),
     "q4mi_plain_stream_probe": (_c.c_bool, [_vp, _c.c_uint64, _u32]),
+    "q4mi_mmq_ab_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
 }
 
 _lib = None
