@@ -173,6 +173,22 @@ bool q4_hip_moe_exec_staged(const uint8_t *base, uint64_t stride, uint32_t gt, u
  * q4_hip_route_pf (src/q4.h:1278-1280, src/q4_rocm.cu:6383-6549). */
 bool q4_hip_route_pf(const float *d_rlog, int32_t *d_ids, float *d_wts, uint32_t n_tok,
                      uint32_t n_exp, uint32_t topk);
+/* Device routing of a decode / verify batch, the reference's entry
+ * (src/q4.h:1285-1294, src/q4_rocm.cu:6106-6283, called from
+ * src/q4_moe.c:2439): per token t < n_tok the softmax top-k of
+ * d_rlog[t][n_exp] (bit-exact with q4_hip_route_pf), each pick mapped
+ * through devtab (expert -> arena slot, < 0 = not resident).  Hits: slots
+ * and renormalised weights at d_es/d_ew[t*64 + i], count d_nh[t] (the device
+ * lists q4_hip_moe_exec_win / _dev read).  Misses: published through `mail`,
+ * the reference's q4_mail_t prefix (ids/wts/rk in token order, n, ntok,
+ * tn[8], hs[8*16] hit slots, hn[8], routed[16] and rseq when d_rseq is
+ * given, then seq = ++*d_seq).  With every expert resident the miss list is
+ * empty.  d_prof (optional): [0] += the kernel's wall-clock ticks (100 MHz),
+ * [1] += 1.  n_exp <= 1024, n_tok 1..8, topk 1..16, n_tok * topk <= 64. */
+bool q4_hip_route_dev_n(const float *d_rlog, const int32_t *devtab, int32_t *d_es, float *d_ew,
+                        int32_t *d_nh, void *mail, unsigned long long *d_seq,
+                        unsigned long long *d_rseq, unsigned long long *d_prof,
+                        uint32_t n_exp, uint32_t topk, uint32_t n_tok);
 /* Single token variants (src/q4.h:1414-1418, src/q4_rocm.cu:12703-12789). */
 bool q4_hip_softmax_topk_launch(const float *d_logits, uint32_t n, uint32_t k, int32_t *d_ids,
                                 float *d_wts);
@@ -203,12 +219,14 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
  * expert's gate applied to its separately computed output, one launch.
  * Replaces q4_hip_sgate_axpy (src/q4.h:1129-1131, src/q4_rocm.cu:15775-15800;
  * src/q4_moe.c:2177).  The dot is q4mi_moe_route's fixed order (so sg has the
- * same bits as its d_sg).  n % 256 == 0, d_w and d_x 16-byte aligned. */
+ * same bits as its d_sg) for n % 256 == 0 and 16-byte aligned d_w, d_x;
+ * any other n or alignment adds the remaining elements lane-strided (any n
+ * >= 1, as the reference). */
 bool q4_hip_sgate_axpy(float *d_y, const float *d_sh, const float *d_w, const float *d_x,
                        uint32_t n, uint32_t n_tok);
 /* *out = sigmoid(a . b) (the one-token sgate scalar).  Replaces
- * q4_hip_dot_sigmoid (src/q4.h:975-976, src/q4_rocm.cu:4890).  n % 256 == 0,
- * a and b 16-byte aligned. */
+ * q4_hip_dot_sigmoid (src/q4.h:975-976, src/q4_rocm.cu:4890).  Any n >= 1
+ * and alignment, the dot in q4_hip_sgate_axpy's order. */
 bool q4_hip_dot_sigmoid(const float *a, const float *b, float *out, uint32_t n);
 /* Stable expert pack per token group: the host order of src/q4_moe.c:
  * 3404-3451 (the reference's GPU assign_pf_k orders by atomic arrival).

@@ -42,6 +42,12 @@ bool q4mi_plain_stream_probe(const void *src, uint64_t bytes, uint32_t unroll);
  * 128 outputs over `groups` (a multiple of 8) 32-value groups, operands in
  * LDS; *ops = the launch's integer ops, for a caller-timed rate. */
 bool q4mi_mmq_ab_probe(int kind, uint32_t groups, uint64_t *ops);
+/* Library device allocations made so far (every allocating path counts). */
+uint64_t q4mi_alloc_count(void);
+/* The scratch grow policy (no growth inside a stream capture; an outgrown
+ * buffer is retired, not freed) run on host fakes without a device; 1 =
+ * every case behaves as documented. */
+int q4mi_grow_selftest(void);
 
 #ifdef __cplusplus
 }

@@ -871,6 +871,7 @@ __global__ __launch_bounds__(256, 2) void mmq_k(MmqArgs a) {
     if (ti >= *a.ntiles) return;
     const uint32_t col = mb.col;
     const int32_t rows = tinfo.z;
+    if (rows <= 0) return;                   // an empty tile (a rejected XG record)
     // block-uniform choice of the (branch-free) sub-tile count
     switch (rows > 96 ? 4 : rows > 64 ? 3 : rows > 32 ? 2 : 1) {
     case 4: mmq_tile<TY, FUSED, 4, XG>(a, smem, tinfo, col); break;
@@ -890,15 +891,14 @@ static int4 *g_tiles = nullptr;
 static uint32_t *g_ntiles = nullptr;
 static uint32_t g_tiles_cap = 0;
 
+// The tile list grows by the library's scratch policy (scratch_grow): never
+// inside a stream capture, and a grown-out list stays allocated, so a graph
+// captured before the growth keeps its own list.
 static bool ensure_tiles(uint32_t n) {
     if (g_tiles_cap >= n) return true;
-    if (g_tiles) (void)hipFree(g_tiles);
-    if (!g_ntiles && hipMalloc(&g_ntiles, sizeof(uint32_t)) != hipSuccess) return false;
-    if (hipMalloc(&g_tiles, (size_t)n * sizeof(int4)) != hipSuccess) {
-        g_tiles = nullptr;
-        g_tiles_cap = 0;
+    if (!g_ntiles && !scratch_grow((void **)&g_ntiles, sizeof(uint32_t), "mmq tile count"))
         return false;
-    }
+    if (!scratch_grow((void **)&g_tiles, (size_t)n * sizeof(int4), "mmq tile list")) return false;
     g_tiles_cap = n;
     return true;
 }
@@ -956,11 +956,36 @@ static bool xg_launch(const MmqArgs &a, dim3 grid) {
 // The reference's XG tile table {first routed row, rows (<= 128), slot,
 // expert} -> this kernel's tile entries (slot as the weight index, first
 // row, rows) and the tile count, on the stream (graph-capturable).
+// A record with rows outside 1..128 (the tile height) or a negative slot or
+// first row becomes an empty tile, which the MMQ kernel skips, and sets
+// kStXgTile in g_mmq_status (read by q4mi_device_status).
+static __device__ uint32_t g_mmq_status;
+constexpr uint32_t kStXgTile = 4u;
+
 __global__ void xg_tiles_k(const int32_t *__restrict__ in, uint32_t n, int4 *__restrict__ out,
                            uint32_t *__restrict__ count) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = make_int4(in[4 * i + 2], in[4 * i], in[4 * i + 1], 0);
+    if (i < n) {
+        const int32_t row = in[4 * i], rows = in[4 * i + 1], slot = in[4 * i + 2];
+        const bool ok = rows >= 1 && rows <= MMQ_MB && slot >= 0 && row >= 0;
+        if (!ok) atomicOr(&g_mmq_status, kStXgTile);
+        out[i] = make_int4(ok ? slot : 0, ok ? row : 0, ok ? rows : 0, 0);
+    }
     if (i == 0) *count = n;
+}
+
+// The MMQ status word (kStXgTile), read and optionally cleared after the
+// stream drained (q4mi_device_status).
+uint32_t mmq_status(int clear) {
+    uint32_t v = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_mmq_status), sizeof v, 0, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return 0x80000000u;
+    if (v && clear) {
+        const uint32_t z = 0;
+        (void)hipMemcpyToSymbol(HIP_SYMBOL(g_mmq_status), &z, sizeof z, 0, hipMemcpyHostToDevice);
+    }
+    return v;
 }
 
 __global__ void xg_cvt_k(const float4 *__restrict__ x, half4_t *__restrict__ y, uint64_t n4) {
@@ -1296,6 +1321,7 @@ uint32_t q4_xg_tiles(const uint32_t *ek, const uint32_t *ebase, const int32_t *s
         }
     return n;
 }
+
 
 /* x16[i] = fp16(x[i]), n % 4 == 0. */
 bool q4_xg_cvt(const float *x, void *x16, uint64_t n) {

@@ -75,7 +75,14 @@ static bool zero_fill(void *p, uint64_t bytes) {
 static bool grow(uint8_t *&buf, uint64_t &have, uint64_t need) {
     if (need <= have) return true;
     uint8_t *nb = nullptr;
-    if (hipMalloc(&nb, need) != hipSuccess) {
+    // weight-sized buffers: freed when outgrown (not retired), so growth is
+    // refused inside a capture like every other library allocation
+    if (stream_capturing()) {
+        set_error("q4_mmq_wbuf: growing to %llu bytes cannot happen inside a stream capture",
+                  (unsigned long long)need);
+        return false;
+    }
+    if (!lib_malloc((void **)&nb, need)) {
         set_error("q4_mmq_wbuf: hipMalloc(%llu) failed", (unsigned long long)need);
         return false;
     }

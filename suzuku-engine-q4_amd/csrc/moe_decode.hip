@@ -53,7 +53,7 @@ static unsigned long long *g_trace = nullptr;
 #endif
 
 bool moe_warm(uint32_t n_ff) {
-    if (!g_plan && hipMalloc(&g_plan, sizeof(Plan)) != hipSuccess) {
+    if (!g_plan && !lib_malloc((void **)&g_plan, sizeof(Plan))) {
         set_error("moe: plan buffer allocation failed");
         return false;
     }
@@ -222,6 +222,7 @@ static bool stage_ready() {
         set_error("q4_hip_moe_stage: pinned allocation failed");
         return false;
     }
+    note_alloc();
     if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess) {
         (void)hipHostFree(p);
         set_error("q4_hip_moe_stage: no device alias for the staging list");
@@ -286,6 +287,7 @@ uint32_t q4mi_device_status(int clear) {
         return 0x80000000u;
     }
     v |= moe_fmt_status(clear);
+    v |= mmq_status(clear);
     if (v) set_error("%s", q4mi_status_text(v));
     if (v && clear) {
         const uint32_t z = 0;

@@ -4,6 +4,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <vector>
+
 #include "../../include/q4mi.h"
 #ifdef Q4MI_MEASURE
 #include "../../include/q4mi_measure.h"
@@ -27,6 +29,42 @@ struct Scratch {
     size_t xq_elems = 0;
 };
 Scratch &lib_scratch();
+
+// Grow policy of every library scratch buffer that a captured graph can
+// reference (decode partials, GEMV activations, MMQ tile list, pack
+// histograms):
+//   - no growth while the library stream is being captured: an allocation
+//     there would not replay, so the call fails with GrowCapturing and the
+//     caller sizes the scratch eagerly first (the warm entry points);
+//   - a grown buffer's predecessor is retired, not freed: a graph captured
+//     before the growth keeps launching on it, so it must stay valid for the
+//     life of the process (the retired bytes stay below the sum of every
+//     size asked for, and growth is rare: the warm entry points size the
+//     scratch once).
+// The hooks are parameters so the policy runs without a device in a test.
+enum GrowResult { GrowOk = 0, GrowCapturing = 1, GrowNoMemory = 2 };
+template <class Capturing, class Alloc>
+inline GrowResult grow_policy(void **p, size_t bytes, Capturing capturing, Alloc alloc,
+                              std::vector<void *> &retired) {
+    if (capturing()) return GrowCapturing;
+    void *n = nullptr;
+    if (!alloc(&n, bytes) || !n) return GrowNoMemory;
+    if (*p) retired.push_back(*p);
+    *p = n;
+    return GrowOk;
+}
+// The device version (library stream, hipMalloc); sets the error text.
+bool scratch_grow(void **p, size_t bytes, const char *what);
+// Every library allocation goes through lib_malloc, which counts them
+// (the measurement build reports the count, q4mi_alloc_count).
+bool lib_malloc(void **p, size_t bytes);
+uint64_t alloc_count();
+void note_alloc();   // counts an allocation made outside lib_malloc (pinned host memory)
+bool stream_capturing();
+// Status word of the MMQ kernels (rejected XG tile records), for
+// q4mi_device_status.
+uint32_t mmq_status(int clear);
+
 bool ensure_pd(size_t floats);
 bool ensure_tickets(size_t n);
 bool ensure_xq(size_t elems);

@@ -9,6 +9,8 @@
 //   reduce_expert_k                      src/q4_rocm.cu:15739-15750
 // The reference's own GPU pack orders rows inside an expert by atomic
 // arrival; this one reproduces the host's stable (t, k) order exactly.
+#include <stddef.h>
+
 #include "q4mi_common.h"
 #include "q4mi_internal.h"
 
@@ -48,30 +50,24 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
 // weight sg[t] (or 1 when sg is null), and nh[t] (when given) = topk + 1
 // (else topk): the per-token device lists of q4_hip_moe_exec_win /
 // q4_hip_moe_exec_dev.
-__global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits, uint32_t n_tok,
-                                               uint32_t n_exp, uint32_t topk,
-                                               int32_t *__restrict__ ids,
-                                               float *__restrict__ wts, uint32_t ostride,
-                                               int32_t shared, const float *__restrict__ sg,
-                                               int32_t *__restrict__ nh) {
-    __shared__ int32_t s_id[4][64];
-    __shared__ float s_p[4][64];
-    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t t = blockIdx.x * 4 + w;
-    if (t >= n_tok) return;
-    const float *lg = logits + (size_t)t * n_exp;
-    float v[8];
+// One wave's softmax + top-k of one token's logits (NJ logits per lane, so
+// up to 64 * NJ experts): picks in rank order land in s_id[0..tk), their
+// probabilities in s_p; returns tk = min(topk, n_exp).
+template <int NJ>
+__device__ inline uint32_t route_wave(const float *__restrict__ lg, uint32_t n_exp, uint32_t topk,
+                                      uint32_t lane, int32_t *s_id, float *s_p) {
+    float v[NJ];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NJ; j++) {
         const uint32_t i = lane + 64u * j;
         v[j] = i < n_exp ? lg[i] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
     mx = key2f(wave_max_u32(f2key(mx)));   // DPP tree, no LDS round trips
-    float e[8], s = 0.f;
+    float e[NJ], s = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NJ; j++) {
         e[j] = (lane + 64u * j) < n_exp ? expf(v[j] - mx) : 0.f;
         s += e[j];
     }
@@ -79,19 +75,19 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
     const float inv = s > 0.f ? __fdiv_rn(1.f, s) : 0.f;
     uint32_t alive = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+    for (int j = 0; j < NJ; j++)
         if ((lane + 64u * j) < n_exp) alive |= 1u << j;
     const uint32_t tk = topk < n_exp ? topk : n_exp;
     // p >= 0, so its key is its bit pattern with the top bit set (a live
     // zero still outranks a dead entry's key 0)
-    uint32_t pk[8];
+    uint32_t pk[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; j++) pk[j] = __float_as_uint(e[j] * inv) | 0x80000000u;
+    for (int j = 0; j < NJ; j++) pk[j] = __float_as_uint(e[j] * inv) | 0x80000000u;
     for (uint32_t k = 0; k < tk; k++) {
         // this lane's best alive entry: largest key, smallest index on ties
         uint32_t bk = 0, bj = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < NJ; j++) {
             const uint32_t key = (alive & (1u << j)) ? pk[j] : 0u;
             if (key > bk) {
                 bk = key;
@@ -107,14 +103,48 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
             alive &= ~(1u << j);
             float pe = 0.f;
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++)
+            for (int jj = 0; jj < NJ; jj++)
                 if ((uint32_t)jj == j) pe = e[jj];
-            s_id[w][k] = (int32_t)wi;
-            s_p[w][k] = pe * inv;
+            s_id[k] = (int32_t)wi;
+            s_p[k] = pe * inv;
         }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    return tk;
+}
+
+// Renormalized weight of pick k: p_k * (1 / sum of the tk picked p, summed
+// in rank order), as q4_topk(renorm) computes it.
+__device__ inline float route_inv_sum(const float *s_p, uint32_t tk) {
+    float sk = 0.f;
+    for (uint32_t k = 0; k < tk; k++) sk += s_p[k];
+    return sk > 0.f ? __fdiv_rn(1.f, sk) : 0.f;
+}
+
+// One wave per token; up to 512 experts (8 per lane), k <= 64.
+// Ranking uses the rounded probabilities p_i = e_i * (1/sum e) with the
+// lower index winning ties, as q4_topk does (src/q4_quant.c:728-750): two
+// different logits whose probabilities round to the same value (near-equal
+// logits, or probabilities that underflow to 0) go to the lower index.
+// Weights: p_i * (1/sum of the k picked p, in rank order).
+// Output row t of ids/wts starts at t * ostride (ostride >= topk).  With
+// shared >= 0 one more entry follows the topk picks: expert `shared` with
+// weight sg[t] (or 1 when sg is null), and nh[t] (when given) = topk + 1
+// (else topk): the per-token device lists of q4_hip_moe_exec_win /
+// q4_hip_moe_exec_dev.
+__global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits, uint32_t n_tok,
+                                               uint32_t n_exp, uint32_t topk,
+                                               int32_t *__restrict__ ids,
+                                               float *__restrict__ wts, uint32_t ostride,
+                                               int32_t shared, const float *__restrict__ sg,
+                                               int32_t *__restrict__ nh) {
+    __shared__ int32_t s_id[4][64];
+    __shared__ float s_p[4][64];
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * 4 + w;
+    if (t >= n_tok) return;
+    const uint32_t tk = route_wave<8>(logits + (size_t)t * n_exp, n_exp, topk, lane, s_id[w], s_p[w]);
     float sk = 0.f;
     for (uint32_t k = 0; k < tk; k++) sk += s_p[w][k];
     const float inv2 = sk > 0.f ? __fdiv_rn(1.f, sk) : 0.f;
@@ -128,6 +158,104 @@ __global__ __launch_bounds__(256) void route_k(const float *__restrict__ logits,
             wts[(size_t)t * ostride + topk] = sg ? sg[t] : 1.f;
         }
         if (nh) nh[t] = (int32_t)(topk + (shared >= 0 ? 1u : 0u));
+    }
+}
+
+// ------------------------------------------------- device routing, verify
+// The reference's device-side decode routing (q4_hip_route_dev_n,
+// src/q4_rocm.cu:6106-6283): per token the softmax top-k of route_wave, the
+// picks mapped through devtab (expert -> arena slot, < 0 = not resident),
+// hits compacted into the token's device list (slots at t * 64, count in
+// nh[t]), misses published through the engine's mailbox in token order.
+// The mailbox layout is the reference's q4_mail_t prefix (its host mirror is
+// moe_mail_t, src/q4_moe.c:368-386); seq is the last field and is bumped
+// last.
+struct RouteMail {
+    int32_t ids[64];      // misses, token-major
+    float wts[64];
+    uint32_t n;           // miss count
+    uint32_t ntok;
+    uint32_t tn[8];       // misses of token t
+    int32_t hs[8 * 16];   // token t's hit slots
+    uint32_t hn[8];       // hits of token t
+    uint8_t rk[64];       // each miss's rank in its token's top-k
+    int32_t routed[16];   // token 0's top-k (profile channel)
+    unsigned long long rseq;
+    unsigned long long seq;
+};
+static_assert(offsetof(RouteMail, n) == 512 && offsetof(RouteMail, hs) == 552 &&
+                  offsetof(RouteMail, rk) == 1096 && offsetof(RouteMail, routed) == 1160 &&
+                  offsetof(RouteMail, rseq) == 1224 && offsetof(RouteMail, seq) == 1232,
+              "mailbox layout of the reference engine");
+
+template <int NJ>
+__global__ __launch_bounds__(512) void route_dev_n_k(
+    const float *__restrict__ rlog, const int32_t *__restrict__ devtab, int32_t *__restrict__ es,
+    float *__restrict__ ew, int32_t *__restrict__ nh, RouteMail *__restrict__ mail,
+    unsigned long long *seq, unsigned long long *rseq, unsigned long long *prof,
+    uint32_t n_exp, uint32_t topk, uint32_t n_tok) {
+    __shared__ int32_t s_id[8][64];
+    __shared__ float s_p[8][64];
+    __shared__ int32_t s_mid[8][16];
+    __shared__ float s_mwt[8][16];
+    __shared__ uint32_t s_mrk[8][16];
+    __shared__ uint32_t s_tn[8];
+    const unsigned long long t0 = wall_clock64();
+    const uint32_t t = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (t < n_tok) {
+        const uint32_t tk = route_wave<NJ>(rlog + (size_t)t * n_exp, n_exp, topk, lane, s_id[t], s_p[t]);
+        const float inv = route_inv_sum(s_p[t], tk);
+        const bool pick = lane < tk;
+        const int32_t id = pick ? s_id[t][lane] : -1;
+        const float wq = pick ? s_p[t][lane] * inv : 0.f;
+        const int32_t slot = id >= 0 ? devtab[id] : -1;
+        const uint64_t hitm = __ballot(pick && slot >= 0), missm = __ballot(pick && slot < 0);
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint32_t hr = (uint32_t)__popcll(hitm & below), mr = (uint32_t)__popcll(missm & below);
+        if (pick && slot >= 0) {
+            es[(size_t)t * 64 + hr] = slot;
+            ew[(size_t)t * 64 + hr] = wq;
+            mail->hs[t * 16 + hr] = slot;
+        } else if (pick) {
+            s_mid[t][mr] = id;
+            s_mwt[t][mr] = wq;
+            s_mrk[t][mr] = lane;
+        }
+        if (t == 0 && rseq && lane < 16) mail->routed[lane] = pick ? id : 0;
+        if (lane == 0) {
+            nh[t] = (int32_t)__popcll(hitm);
+            s_tn[t] = (uint32_t)__popcll(missm);
+            mail->hn[t] = (uint32_t)__popcll(hitm);
+        }
+    }
+    __syncthreads();
+    if (t != 0) return;
+    uint32_t nm = 0;
+    for (uint32_t u = 0; u < n_tok; u++) {
+        const uint32_t c = s_tn[u];
+        if (lane < c) {
+            mail->ids[nm + lane] = s_mid[u][lane];
+            mail->wts[nm + lane] = s_mwt[u][lane];
+            mail->rk[nm + lane] = (uint8_t)s_mrk[u][lane];
+        }
+        nm += c;
+    }
+    if (lane < 8) {
+        mail->tn[lane] = lane < n_tok ? s_tn[lane] : 0u;
+        if (lane >= n_tok) mail->hn[lane] = 0u;
+    }
+    if (lane == 0) {
+        mail->ntok = n_tok;
+        mail->n = nm;
+        if (rseq) mail->rseq = ++(*rseq);
+        // the engine reads the mailbox through a copy ordered after this
+        // kernel on the stream, so the kernel's end makes every field
+        // visible before seq is seen
+        mail->seq = ++(*seq);
+        if (prof) {
+            prof[0] += wall_clock64() - t0;
+            prof[1] += 1;
+        }
     }
 }
 
@@ -296,6 +424,21 @@ bool route_launch(const float *lg, int32_t *ids, float *wts, uint32_t n_tok, uin
     return launch_ok("route_k");
 }
 
+bool route_dev_n_launch(const float *rlog, const int32_t *devtab, int32_t *es, float *ew,
+                        int32_t *nh, void *mail, unsigned long long *seq, unsigned long long *rseq,
+                        unsigned long long *prof, uint32_t n_exp, uint32_t topk, uint32_t n_tok) {
+    RouteMail *m = (RouteMail *)mail;
+    if (n_exp <= 512)
+        route_dev_n_k<8><<<dim3(1), dim3(64 * n_tok), 0, stream()>>>(rlog, devtab, es, ew, nh, m,
+                                                                  seq, rseq, prof, n_exp, topk,
+                                                                  n_tok);
+    else
+        route_dev_n_k<16><<<dim3(1), dim3(64 * n_tok), 0, stream()>>>(rlog, devtab, es, ew, nh, m,
+                                                                   seq, rseq, prof, n_exp, topk,
+                                                                   n_tok);
+    return launch_ok("route_dev_n_k");
+}
+
 bool route_list_launch(const float *lg, int32_t *ids, float *wts, int32_t *nh, uint32_t n_tok,
                        uint32_t n_exp, uint32_t topk, uint32_t ostride, int32_t shared,
                        const float *sg) {
@@ -316,13 +459,7 @@ bool assign_launch(const int32_t *ids, const float *wts, int32_t *a_tok, int32_t
     const uint32_t nch = (gsz * topk + kPackCh - 1) / kPackCh;
     const size_t words = (size_t)n_g * nch * 512;
     if (g_hist_words < words) {
-        uint32_t *n = nullptr;
-        if (hipMalloc(&n, words * 4) != hipSuccess) {
-            set_error("pack: scratch allocation failed");
-            return false;
-        }
-        if (g_hist) (void)hipFree(g_hist);
-        g_hist = n;
+        if (!scratch_grow((void **)&g_hist, words * 4, "pack histograms")) return false;
         g_hist_words = words;
     }
     pack_hist_k<<<dim3(nch, n_g), dim3(512), 0, stream()>>>(ids, g_hist, gsz, topk, n_exp, n_tok,
@@ -350,6 +487,27 @@ extern "C" {
 
 /* Per-token softmax + top-k (renormalised) over n_exp <= 512 logits,
  * topk 1..64: ids/wts [n_tok][topk] (device). */
+/* Device routing of a decode or verify batch (reference signature,
+ * src/q4.h:1289-1294): per token the softmax top-k of d_rlog[t][n_exp]
+ * (bit-exact with q4_hip_route_pf), picks mapped through devtab; hits go to
+ * d_es/d_ew at t*64 (count d_nh[t]), misses to the mailbox, whose seq (and
+ * rseq when d_rseq is given) is bumped from the device counters.  All
+ * experts resident (devtab[e] >= 0 for every e) leaves the miss list empty.
+ * false (nothing launched): a null argument, n_exp > 1024, n_tok outside
+ * 1..8, topk outside 1..16 or n_tok * topk > 64. */
+bool q4_hip_route_dev_n(const float *d_rlog, const int32_t *devtab, int32_t *d_es, float *d_ew,
+                        int32_t *d_nh, void *mail, unsigned long long *d_seq,
+                        unsigned long long *d_rseq, unsigned long long *d_prof,
+                        uint32_t n_exp, uint32_t topk, uint32_t n_tok) {
+    if (!d_rlog || !devtab || !d_es || !d_ew || !d_nh || !mail || !d_seq || !n_exp ||
+        n_exp > 1024 || !n_tok || n_tok > 8 || !topk || topk > 16 || n_tok * topk > 64) {
+        set_error("q4_hip_route_dev_n: bad arguments");
+        return false;
+    }
+    return route_dev_n_launch(d_rlog, devtab, d_es, d_ew, d_nh, mail, d_seq, d_rseq, d_prof,
+                              n_exp, topk, n_tok);
+}
+
 bool q4_hip_route_pf(const float *d_rlog, int32_t *d_ids, float *d_wts, uint32_t n_tok,
                      uint32_t n_exp, uint32_t topk) {
     if (!d_rlog || !d_ids || !d_wts || !n_tok || !n_exp || n_exp > 512u || !topk ||
@@ -373,8 +531,8 @@ bool q4_hip_softmax_topk(const float *d_logits, uint32_t n, uint32_t k, int32_t 
     static int32_t *d_ids = nullptr;
     static float *d_w = nullptr;
     if (!d_ids) {
-        if (hipMalloc(&d_ids, 64 * sizeof(int32_t)) != hipSuccess ||
-            hipMalloc(&d_w, 64 * sizeof(float)) != hipSuccess) {
+        if (!lib_malloc((void **)&d_ids, 64 * sizeof(int32_t)) ||
+            !lib_malloc((void **)&d_w, 64 * sizeof(float))) {
             set_error("q4_hip_softmax_topk: hipMalloc failed");
             return false;
         }

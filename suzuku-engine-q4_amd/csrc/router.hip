@@ -111,12 +111,17 @@ __global__ __launch_bounds__(256) void router_gemv_k(const uint8_t *__restrict__
     }
 }
 
-// One wave's dot of w and x (K % 256 == 0) in the router's fixed order;
-// every lane returns the total.
+// One wave's dot of w and x in the router's fixed order; every lane returns
+// the total.  With both vectors 16-byte aligned the first K - K % 256
+// elements go by float4 as above; the rest (or all of K when either vector
+// is not 16-byte aligned) are taken lane-strided -- lane l adds elements
+// b + l, b + l + 64, ... in order -- before the butterfly.
 __device__ inline float wave_dot(const float *__restrict__ w, const float *__restrict__ x,
                                  uint32_t K, uint32_t lane) {
     float acc = 0.f;
-    for (uint32_t i = 0; i < K / 256; i++) {
+    const bool vec = (((uintptr_t)w | (uintptr_t)x) & 15u) == 0;
+    const uint32_t kv = vec ? K / 256 * 256 : 0u;
+    for (uint32_t i = 0; i < kv / 256; i++) {
         const float4 a = ((const float4 *)w)[64 * i + lane];
         const float4 b = ((const float4 *)x)[64 * i + lane];
         acc = fmaf(a.x, b.x, acc);
@@ -124,6 +129,7 @@ __device__ inline float wave_dot(const float *__restrict__ w, const float *__res
         acc = fmaf(a.z, b.z, acc);
         acc = fmaf(a.w, b.w, acc);
     }
+    for (uint32_t i = kv + lane; i < K; i += 64) acc = fmaf(w[i], x[i], acc);
     return xor_sum64(acc);
 }
 
@@ -216,8 +222,7 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
  * (see include/q4mi.h). */
 bool q4_hip_sgate_axpy(float *d_y, const float *d_sh, const float *d_w, const float *d_x,
                        uint32_t n, uint32_t n_tok) {
-    if (!d_y || !d_sh || !d_w || !d_x || !n || !n_tok || n % 256 ||
-        (((uintptr_t)d_w | (uintptr_t)d_x) & 15u)) {
+    if (!d_y || !d_sh || !d_w || !d_x || !n || !n_tok) {
         set_error("q4_hip_sgate_axpy: bad arguments");
         return false;
     }
@@ -228,7 +233,7 @@ bool q4_hip_sgate_axpy(float *d_y, const float *d_sh, const float *d_w, const fl
 
 /* *out = sigmoid(a . b), one launch (see include/q4mi.h). */
 bool q4_hip_dot_sigmoid(const float *a, const float *b, float *out, uint32_t n) {
-    if (!a || !b || !out || !n || n % 256 || (((uintptr_t)a | (uintptr_t)b) & 15u)) {
+    if (!a || !b || !out || !n) {
         set_error("q4_hip_dot_sigmoid: bad arguments");
         return false;
     }

@@ -69,6 +69,7 @@ _SIGS = {
     "q4_hip_moe_exec_staged": (_b, [_vp, _u64, _u32, _u64, _u32, _u64, _u32, _u64, _vp, _vp,
                                     _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_route_pf": (_b, [_vp, _vp, _vp, _u32, _u32, _u32]),
+    "q4_hip_route_dev_n": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "q4_hip_softmax_topk_launch": (_b, [_vp, _u32, _u32, _vp, _vp]),
     "q4_hip_softmax_topk": (_b, [_vp, _u32, _u32, _vp, _vp]),
     "q4mi_moe_route": (_b, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp,
@@ -120,6 +121,8 @@ _MEAS_SIGS = {
     "q4mi_stream_probe": (_c.c_bool, [_vp, _u32, _u32, _c.POINTER(_c.c_uint64)]),
     "q4mi_plain_stream_probe": (_c.c_bool, [_vp, _c.c_uint64, _u32]),
     "q4mi_mmq_ab_probe": (_c.c_bool, [_c.c_int, _u32, _c.POINTER(_c.c_uint64)]),
+    "q4mi_alloc_count": (_c.c_uint64, []),
+    "q4mi_grow_selftest": (_c.c_int, []),
 }
 
 _lib = None

@@ -128,3 +128,49 @@ def test_status_text():
     assert "producer" in t2 and "consumer" not in t2
     assert "consumer, producer" in L.q4mi_status_text(3).decode()
     assert "not readable" in L.q4mi_status_text(0x80000000).decode()
+
+
+def test_grow_policy_selftest():
+    """Library scratch grows by one policy: never inside a stream capture (the
+    call fails instead), and an outgrown buffer is retired, not freed, so a
+    graph captured before the growth keeps valid memory.  The measurement
+    build runs the policy on host fakes (no device needed)."""
+    M = q4mi.meas()
+    assert M.q4mi_grow_selftest() == 1
+
+
+def test_status_text_xg_tiles():
+    L = q4mi.lib()
+    t = L.q4mi_status_text(4).decode()
+    assert "XG tile record" in t and "skipped" in t and "bounded wait" not in t
+    t5 = L.q4mi_status_text(5).decode()
+    assert "consumer" in t5 and "XG tile" in t5
+
+
+def test_xg_tiles_host_table():
+    """q4_xg_tiles (host code, no device): the reference's tile record
+    {first routed row, rows, slot, expert}, every tile at most 128 rows, the
+    rows of each expert covered once in order; a too-small capacity gives 0."""
+    import ctypes
+    import numpy as np
+    L = q4mi.lib()
+    rng = np.random.default_rng(3)
+    E = 40
+    ek = rng.integers(0, 400, E).astype(np.uint32)
+    ek[[3, 9]] = [128, 129]
+    eb = np.concatenate([[0], np.cumsum(ek)[:-1]]).astype(np.uint32)
+    slot = rng.permutation(E).astype(np.int32)
+    cap = int(L.q4_xg_tile_cap(int(ek.sum()), E))
+    out = np.full(4 * cap, -1, np.int32)
+    n = L.q4_xg_tiles(ek.ctypes.data, eb.ctypes.data, slot.ctypes.data, E, out.ctypes.data, cap)
+    tiles = out[:4 * n].reshape(n, 4)
+    assert n == int(sum((int(c) + 127) // 128 for c in ek))
+    assert tiles[:, 1].max() <= 128 and tiles[:, 1].min() >= 1
+    for e in range(E):
+        te = tiles[tiles[:, 3] == e]
+        assert te[:, 1].sum() == ek[e]
+        assert np.all(te[:, 2] == slot[e])
+        assert np.array_equal(te[:, 0], eb[e] + 128 * np.arange(len(te)))
+    small = np.zeros(4 * (n - 1), np.int32)
+    assert L.q4_xg_tiles(ek.ctypes.data, eb.ctypes.data, slot.ctypes.data, E, small.ctypes.data,
+                         n - 1) == 0

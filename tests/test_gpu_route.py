@@ -165,3 +165,86 @@ def test_expert_reduce(gpu):
             if rsrc[t, j] >= 0:
                 ref[t] += rw[t, j] * pd[rsrc[t, j]].astype(np.float64)
     assert np.abs(host(y) - ref).max() < 1e-4
+
+
+MAIL_BYTES = 1240           # the reference mailbox prefix copied to the host (through seq)
+
+
+def mail_fields(raw):
+    """Fields of the reference's q4_mail_t prefix (src/q4_moe.c:368-386)."""
+    b = raw.tobytes()
+    i32 = lambda o, n: np.frombuffer(b, np.int32, n, o)
+    return {"ids": i32(0, 64), "wts": np.frombuffer(b, np.float32, 64, 256),
+            "n": int(i32(512, 1)[0]), "ntok": int(i32(516, 1)[0]), "tn": i32(520, 8),
+            "hs": i32(552, 128), "hn": i32(1064, 8), "rk": np.frombuffer(b, np.uint8, 64, 1096),
+            "routed": i32(1160, 16), "rseq": int(np.frombuffer(b, np.uint64, 1, 1224)[0]),
+            "seq": int(np.frombuffer(b, np.uint64, 1, 1232)[0])}
+
+
+@pytest.mark.parametrize("T,E,k,resident", [(1, 512, 10, "all"), (4, 512, 10, "all"),
+                                            (4, 512, 10, "half"), (6, 1024, 10, "half"),
+                                            (8, 700, 8, "none")])
+def test_route_dev_n_reference_signature(gpu, oracle, T, E, k, resident):
+    """q4_hip_route_dev_n through the reference's signature (src/q4.h:1289-1294):
+    hits land in the stride-64 device lists as slots, misses in the mailbox
+    in token order with their ranks, seq / rseq bumped once per call; ids and
+    weights are q4_topk's (the oracle), ids bit-exact."""
+    import torch
+    L = gpu
+    rng = np.random.default_rng(T * 31 + E)
+    lg = synth.logits(rng, T, E, zipf=False)
+    if resident == "all":
+        devtab = np.arange(E, dtype=np.int32)[::-1].copy()       # slot = E - 1 - id
+    elif resident == "half":
+        devtab = np.where(np.arange(E) % 2 == 0, np.arange(E) // 2, -1).astype(np.int32)
+    else:
+        devtab = np.full(E, -1, np.int32)
+    d_lg, d_tab = dev(lg), dev(devtab)
+    es = torch.full((T, 64), -9, dtype=torch.int32, device="cuda")
+    ew = torch.zeros((T, 64), dtype=torch.float32, device="cuda")
+    nh = torch.full((T,), -9, dtype=torch.int32, device="cuda")
+    mail = torch.zeros(1280, dtype=torch.uint8, device="cuda")
+    seq = torch.tensor([41], dtype=torch.uint64, device="cuda")
+    rseq = torch.tensor([7], dtype=torch.uint64, device="cuda")
+    prof = torch.zeros(2, dtype=torch.uint64, device="cuda")
+    P = q4mi.ptr
+    for call in range(2):
+        q4mi.check(L.q4_hip_route_dev_n(P(d_lg), P(d_tab), P(es), P(ew), P(nh), P(mail), P(seq),
+                                        P(rseq), P(prof), E, k, T), "q4_hip_route_dev_n")
+    es_h, ew_h, nh_h = host(es), host(ew), host(nh)
+    m = mail_fields(host(mail)[:MAIL_BYTES])
+    oid, ow = oracle.softmax_topk(lg, k)
+    assert m["seq"] == 43 and m["rseq"] == 9 and int(host(prof)[1]) == 2
+    assert m["ntok"] == T
+    miss_ids, miss_w, miss_rk = [], [], []
+    for t in range(T):
+        slots = devtab[oid[t]]
+        hit = slots >= 0
+        nhit = int(hit.sum())
+        assert nh_h[t] == nhit and m["hn"][t] == nhit and m["tn"][t] == k - nhit
+        assert np.array_equal(es_h[t, :nhit], slots[hit])
+        assert np.array_equal(m["hs"][16 * t:16 * t + nhit], slots[hit])
+        assert np.allclose(ew_h[t, :nhit], ow[t][hit], rtol=1e-6, atol=1e-9)
+        assert np.all(es_h[t, nhit:] == -9)                     # nothing past the hits
+        miss_ids += list(oid[t][~hit])
+        miss_w += list(ow[t][~hit])
+        miss_rk += list(np.nonzero(~hit)[0])
+    n = len(miss_ids)
+    assert m["n"] == n
+    assert np.array_equal(m["ids"][:n], np.array(miss_ids, np.int32))
+    assert np.allclose(m["wts"][:n], np.array(miss_w, np.float32), rtol=1e-6, atol=1e-9)
+    assert np.array_equal(m["rk"][:n], np.array(miss_rk, np.uint8))
+    assert np.all(m["tn"][T:] == 0) and np.all(m["hn"][T:] == 0)
+    assert np.array_equal(m["routed"][:k], oid[0]) and np.all(m["routed"][k:] == 0)
+
+
+def test_route_dev_n_rejects(gpu):
+    """The reference's bounds: n_tok * topk <= 64, topk <= 16, n_exp <= 1024,
+    n_tok <= 8 -> false before any launch."""
+    import torch
+    L = gpu
+    z = torch.zeros(8 * 2048, dtype=torch.float32, device="cuda")
+    P = q4mi.ptr
+    for E, k, T in ((512, 10, 7), (512, 17, 1), (1025, 4, 1), (512, 4, 9), (512, 0, 1)):
+        assert not L.q4_hip_route_dev_n(P(z), P(z), P(z), P(z), P(z), P(z), P(z), None, None,
+                                        E, k, T)

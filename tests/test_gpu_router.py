@@ -169,7 +169,34 @@ def test_sgate_axpy_and_dot_sigmoid(gpu, oracle):
     want = y0 + osg[:, None] * sh
     assert rel_err(host(y), want) <= 1e-5
     assert abs(float(host(out)[0]) - osg[2]) <= 1e-6 * abs(osg[2])
-    assert not gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), 1000, 1)
+    assert not gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), q4mi.ptr(y), 0, 1)
+
+
+@pytest.mark.parametrize("n,off", [(1000, 0), (2048, 1), (77, 3), (4096 + 130, 2)])
+def test_sgate_any_size_and_alignment(gpu, n, off):
+    """Any n and any (float) alignment, as the reference accepts: the gate
+    matches a float64 sigmoid(w . x) to 1e-6 relative, and y += sg * sh to
+    1e-4 (one fp32 rounding of y0 + sg sh against float64, near-cancelling
+    sums included)."""
+    rng = np.random.default_rng(n + off)
+    T = 3
+    g = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, n)).astype(np.float32)
+    sh = rng.standard_normal((T, n)).astype(np.float32)
+    y0 = rng.standard_normal((T, n)).astype(np.float32)
+    # misalign w and x by `off` floats inside padded device buffers
+    dg = dev(np.concatenate([np.zeros(off, np.float32), g]))
+    dx = dev(np.concatenate([np.zeros(off, np.float32), x.ravel()]))
+    y = dev(y0)
+    pw, px = q4mi.ptr(dg) + 4 * off, q4mi.ptr(dx) + 4 * off
+    q4mi.check(gpu.q4_hip_sgate_axpy(q4mi.ptr(y), q4mi.ptr(dev(sh)), pw, px, n, T), "sgate_axpy")
+    out = zeros(1)
+    q4mi.check(gpu.q4_hip_dot_sigmoid(pw, px + 4 * n, q4mi.ptr(out), n), "dot_sigmoid")
+    d = x.astype(np.float64) @ g.astype(np.float64)
+    sg = 1.0 / (1.0 + np.exp(-d))
+    assert abs(float(host(out)[0]) - sg[1]) <= 1e-6 * sg[1]
+    want = y0.astype(np.float64) + sg[:, None] * sh
+    assert rel_err(host(y), want.astype(np.float32)) <= 1e-4
 
 
 def test_routed_window_graph_replays(gpu):
