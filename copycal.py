@@ -1,6 +1,6 @@
 """Copy of a known size, for calibrating HBM byte counters.
 
-`python -m q4mi.copycal [MiB] [reps]` copies a MiB-sized device buffer to
+`python copycal.py [MiB] [reps]` (repo root, beside bench.py) copies a MiB-sized device buffer to
 another `reps` times (torch's device copy kernel).  Under
 `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE) each dispatch should report
 MiB * 1024 KiB; the ratio of the reported to the known size is the factor
