@@ -235,9 +235,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--profile", choices=["decode", "window", "prefill"],
-                    help="a short run of one workload for rocprofv3 (no CPU baseline)")
+    ap.add_argument("--profile", choices=["decode", "window", "prefill", "mmq"],
+                    help="a short run of one workload for rocprofv3 (no CPU baseline); mmq: "
+                         "time the configs[3] prefill's gate/up and down MMQ launches alone "
+                         "(with Q4MI_LIB naming a library variant, its knockouts)")
     args = ap.parse_args()
+    if args.profile == "mmq":
+        sys.stdout.write(json.dumps(bench_mmq_launches()) + "\n")
+        return
     if args.profile:
         args.no_cpu = True
         args.no_prefill = args.profile != "prefill"
@@ -621,6 +626,73 @@ def bench_prefill(L, torch, np, q4mi, synth, args, copies=3, reps=10):
             "weight_GB_per_s": round(wbytes / t / 1e9, 1),
             "note": "whole routed layer incl. route, pack, quantize, SwiGLU, reduce and the "
                     "shared expert; ops = (20480 + 2048) rows x 3 x 2048 x 512 x 2"}
+
+
+def bench_mmq_launches(copies=3, reps=8):
+    """The configs[3] prefill's two MMQ launches timed alone (eager, events
+    on the library stream over `copies` rotating weight arenas): gate/up
+    (routed + shared, fused SwiGLU + q8(h)) and down.  Used with library
+    variants built by `python -m q4mi.build --lib ... --define ...` to
+    attribute the kernels' time (Q4MI_MMQ_KO knockouts)."""
+    import numpy as np
+    import torch
+    import q4mi
+    from q4mi import synth
+    L = q4mi.lib()
+    torch.cuda.set_device(0)
+    q4mi.use_torch_stream(L)
+    T, k, E, H, F = PF_T, PF_K, N_EXP, N_EMBD, N_FF
+    stride, og, ou, od = synth.expert_stride(H, F)
+    rows = T * k
+    rng = np.random.default_rng(99)
+    arenas = [synth.device_iq3s((E + 1) * stride, seed=500 + c) for c in range(copies)]
+    x = torch.randn(T, H, device="cuda")
+    lg = torch.from_numpy(synth.logits(rng, T, E, zipf=True)).cuda()
+    i32 = torch.int32
+    ids, wts = torch.empty(T, k, dtype=i32, device="cuda"), torch.empty(T, k, device="cuda")
+    a_tok = torch.empty(rows + T, dtype=i32, device="cuda")
+    a_tok[rows:] = torch.arange(T, dtype=i32, device="cuda")
+    rsrc = torch.empty(rows, dtype=i32, device="cuda")
+    rw = torch.empty(rows, device="cuda")
+    stg, stgn = torch.empty(512, dtype=i32, device="cuda"), torch.empty(1, dtype=i32, device="cuda")
+    ek = torch.empty(512, dtype=i32, device="cuda")
+    bounds = torch.empty(E + 2, dtype=i32, device="cuda")
+    bounds[E + 1] = rows + T
+    xq = torch.empty(int(L.q4_mmq_q8_bytes(T, H)), dtype=torch.uint8, device="cuda")
+    hq = torch.empty(int(L.q4_mmq_q8_bytes(rows + T, F)), dtype=torch.uint8, device="cuda")
+    pd = torch.empty(rows + T, H, device="cuda")
+    P, TY, chk = q4mi.ptr, q4mi.T_IQ3_S, q4mi.check
+    chk(L.q4_hip_route_pf(P(lg), P(ids), P(wts), T, E, k), "route", L)
+    chk(L.q4mi_assign(P(ids), P(wts), P(a_tok), P(rsrc), P(rw), P(stg), P(stgn), P(ek),
+                      P(bounds), T, k, E, T), "assign", L)
+    chk(L.q4_mmq_quantize(P(x), None, P(xq), TY, H, T), "q8 x", L)
+
+    def gu(c):
+        A = arenas[c].data_ptr()
+        chk(L.q4mi_mmq_gate_up_x(A, A + E * stride, TY, F, H, stride, E, P(xq), T, P(a_tok),
+                                 P(bounds), rows + T, P(hq)), "mmq gate/up", L)
+
+    def dn(c):
+        A = arenas[c].data_ptr()
+        chk(L.q4mi_mmq_mul_id_x(A + od, A + E * stride + od, TY, H, F, stride, E, P(hq),
+                                P(bounds), rows + T, P(pd), H), "mmq down", L)
+
+    def clock(fn):
+        for c in range(copies):
+            fn(c)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for c in range(copies):
+                fn(c)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * copies)
+    res = {"gate_up_us": round(clock(gu), 1), "down_us": round(clock(dn), 1),
+           "library": os.path.basename(q4mi.LIB_PATH)}
+    del arenas
+    return res
 
 
 def bench_prefill_xg(L, torch, np, q4mi, synth, args, copies=3, reps=10):

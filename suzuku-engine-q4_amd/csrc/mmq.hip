@@ -674,11 +674,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         auto scale = [&](int n, const f32x16_t &sacc, float dxv) __attribute__((always_inline)) {
             const int gl = n / NSUB, t = n % NSUB;
             if constexpr (MmqFmt<TY>::kSuper) {
-                if (MMQ_KO(a, 4)) {   // one FMA instead of sixteen
-                    float z = sacc[0];
-#pragma unroll
-                    for (int i = 1; i < 16; i++) z = fmaxf(z, sacc[i]);
-                    inner[t][n & 15] = fmaf(z, dxv, inner[t][n & 15]);
+                if (MMQ_KO(a, 4)) {   // two VALU ops instead of sixteen FMAs
+                    inner[t][n & 15] = fmaf(sacc[0] + sacc[15], dxv, inner[t][n & 15]);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 16; i++) inner[t][i] = fmaf(sacc[i], dxv, inner[t][i]);

@@ -50,6 +50,33 @@ def _link(objs, lib):
     os.replace(tmp, lib)
 
 
+def build_variant(lib, defines, verbose=False):
+    """A measurement-build variant with extra preprocessor defines (e.g. the
+    MMQ timing knockouts, Q4MI_MMQ_KO=bits, or the decode phase trace,
+    Q4MI_TRACE) linked into `lib`; objects go to _build/<lib name>."""
+    tag = os.path.splitext(os.path.basename(lib))[0]
+    odir = os.path.join(OBJ, tag)
+    os.makedirs(odir, exist_ok=True)
+    os.makedirs(os.path.dirname(os.path.abspath(lib)), exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")), key=lambda p: -os.path.getsize(p))
+    extra = ["-DQ4MI_MEASURE"] + ["-D" + d for d in defines]
+
+    def one(src):
+        obj = os.path.join(odir, os.path.basename(src).replace(".hip", ".o"))
+        r = subprocess.run([HIPCC] + FLAGS + extra + ["-c", src, "-o", obj], capture_output=True,
+                           text=True)
+        return obj, r.returncode, r.stderr
+
+    with cf.ThreadPoolExecutor(min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))) as ex:
+        res = list(ex.map(one, srcs))
+    for obj, rc, err in res:
+        if rc != 0:
+            sys.stderr.write(err + "\n")
+            raise RuntimeError("hipcc failed for " + obj)
+    _link([r[0] for r in res], lib)
+    return lib
+
+
 def build(verbose=False, measure=True):
     variants = ["prod", "meas"] if measure else ["prod"]
     for v in variants:
@@ -76,4 +103,13 @@ def build(verbose=False, measure=True):
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    import argparse
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--lib", help="build a measurement variant into this path instead")
+    ap.add_argument("--define", action="append", default=[],
+                    help="NAME[=VALUE] for the variant (repeatable)")
+    args = ap.parse_args()
+    if args.lib:
+        print(build_variant(args.lib, args.define, verbose=True))
+    else:
+        print(build(verbose=True))
