@@ -235,13 +235,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--profile", choices=["decode", "window", "prefill", "mmq"],
+    ap.add_argument("--profile", choices=["decode", "window", "prefill", "mmq", "gemv"],
                     help="a short run of one workload for rocprofv3 (no CPU baseline); mmq: "
                          "time the configs[3] prefill's gate/up and down MMQ launches alone "
-                         "(with Q4MI_LIB naming a library variant, its knockouts)")
+                         "(with Q4MI_LIB naming a library variant, its knockouts); gemv: "
+                         "the configs[0] and configs[4] GEMV lines alone")
     args = ap.parse_args()
     if args.profile == "mmq":
         sys.stdout.write(json.dumps(bench_mmq_launches()) + "\n")
+        return
+    if args.profile == "gemv":
+        sys.stdout.write(json.dumps(bench_gemv_lines()) + "\n")
         return
     if args.profile:
         args.no_cpu = True
@@ -868,6 +872,29 @@ def bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, ti
             "unique_experts": round(float(np.mean(uniq)), 2), "tokens": n_tok,
             "note": "4 tokens, own top-10 each + shared; each unique expert read once; "
                     "graph over the %d-layer stack" % NL}
+
+
+def bench_gemv_lines():
+    """The configs[0] and configs[4] GEMV lines alone (library from Q4MI_LIB
+    when set)."""
+    import numpy as np
+    import torch
+    import q4mi
+    from q4mi import synth
+    L = q4mi.lib()
+    torch.cuda.set_device(0)
+    q4mi.use_torch_stream(L)
+    T = q4mi.T_IQ3_S
+    out = {"library": os.path.basename(q4mi.LIB_PATH)}
+    out["config0_gemv"] = bench_gemv(L, torch, np, q4mi, synth, T, 4096, 4096, 80, 1, "configs[0]")
+    out["config4_lmhead_n1"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936, 2048,
+                                          2, 1, "configs[4]")
+    out["config4_lmhead_n4"] = bench_gemv(L, torch, np, q4mi, synth, q4mi.T_Q8_0, 151936, 2048,
+                                          2, 4, "configs[4]")
+    for v in out.values():
+        if isinstance(v, dict):
+            v.pop("note", None)
+    return out
 
 
 def bench_gemv(L, torch, np, q4mi, synth, ty, rows, K, copies, nt, label, reps=30):

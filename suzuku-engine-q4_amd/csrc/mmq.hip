@@ -556,6 +556,20 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         inner[t] = f32x16_t{};
     }
     const uint32_t arow = 32 * wv + (lane & 31u);    // this lane's weight row in the tile
+    // Byte offsets inside a stage buffer of this lane's B operand chunks
+    // (token row lane % 32 of sub-tile 0; sub-tile t adds 32 rows, a
+    // constant) and of its group scales: loop invariant, so each read is a
+    // per-stage base plus an immediate.
+    const uint32_t l31 = lane & 31u;
+    uint32_t boff[GPS][2];
+#pragma unroll
+    for (uint32_t gl = 0; gl < GPS; gl++)
+#pragma unroll
+        for (uint32_t hf = 0; hf < 2; hf++) {
+            const uint32_t c = 4 * gl + 2 * hf + kh;             // logical 16-byte chunk
+            boff[gl][hf] = 2u * (l31 * KS + 8u * (c ^ (l31 & 7u)));
+        }
+    const uint32_t dxoff = 4u * l31 * GPS;
     issue_stage(0);
     if constexpr (TY == Q4MI_T_IQ3_S) {   // tables (read after the first barrier pair)
 #pragma unroll
@@ -653,20 +667,20 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
         // exact-integer MFMA pair, then one scale FMA per output.  Product
         // n+1's pair is issued before product n's FMAs, so the FMAs never
         // wait on the pair right before them.
-        const _Float16 *actc = actb + buf * kActBuf;
+        const uint8_t *actc8 = (const uint8_t *)(actb + buf * kActBuf);
+        const uint8_t *dxc8 = (const uint8_t *)(dxb + buf * kDxBuf) + dxoff;
         auto prod = [&](int n, float &dxo) __attribute__((always_inline)) {
             const int gl = n / NSUB, t = n % NSUB;
-            const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;   // logical 16-B chunks
-            const uint32_t tok = 32 * t + (lane & 31u);
             half8_t B0, B1;
             if (MMQ_KO(a, 3)) {
+                const uint32_t tok = 32 * t + l31;
                 B0 = half8_t{} + (_Float16)(float)(tok + gl);
                 B1 = half8_t{} + (_Float16)(float)(tok + t);
                 dxo = (float)n;
             } else {
-                B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
-                B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
-                dxo = dxb[buf * kDxBuf + tok * GPS + gl];
+                B0 = *(const half8_t *)(actc8 + boff[gl][0] + 64u * KS * t);
+                B1 = *(const half8_t *)(actc8 + boff[gl][1] + 64u * KS * t);
+                dxo = *(const float *)(dxc8 + 4u * (32u * GPS * t + gl));
             }
             f32x16_t r = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, f32x16_t{}, 0, 0, 0);
             return __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, r, 0, 0, 0);
@@ -696,10 +710,8 @@ __device__ __attribute__((always_inline)) inline void mmq_tile(const MmqArgs a, 
 #pragma unroll
             for (int n = 0; n < (int)GPS * NSUB; n++) {
                 const int gl = n / NSUB, t = n % NSUB;
-                const uint32_t c0 = 4 * gl + kh, c1 = 4 * gl + 2 + kh;
-                const uint32_t tok = 32 * t + (lane & 31u);
-                const half8_t B0 = *(const half8_t *)(actc + tok * KS + 8 * (c0 ^ (tok & 7u)));
-                const half8_t B1 = *(const half8_t *)(actc + tok * KS + 8 * (c1 ^ (tok & 7u)));
+                const half8_t B0 = *(const half8_t *)(actc8 + boff[gl][0] + 64u * KS * t);
+                const half8_t B1 = *(const half8_t *)(actc8 + boff[gl][1] + 64u * KS * t);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][0], B0, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[gl][1], B1, acc[t], 0, 0, 0);
             }
