@@ -12,10 +12,12 @@ namespace q4mi {
 bool quant8_launch(const float *x, const int32_t *ids, uint64_t rows, uint32_t cols,
                    int8_t *q, float *d, int32_t *bs);
 
-// xf (optional): fp32 activations [nt][K], quantized by every block into
-// LDS behind its weight tile (the q8 codes and scales of q8_quant_k, bit for
+// XF: fp32 activations xf [nt][K], quantized by every block into LDS
+// behind its weight tile (the q8 codes and scales of q8_quant_k, bit for
 // bit), so a call needs no separate quantize launch; else xq / xd hold them.
-template <class F, int NT, int TPR, int GPT>
+// (Two instantiations: the in-block quantizer's batched loads take 32
+// registers, which the pre-quantized kernel does not pay for.)
+template <class F, int NT, int TPR, int GPT, bool XF>
 __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uint32_t rows,
                                               uint32_t K, uint32_t rb, uint32_t R,
                                               const float *__restrict__ xf,
@@ -41,8 +43,8 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
     // pre-quantized codes: loaded while the tile copy is in flight
-    if (!xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
-    if (xf) {
+    if constexpr (!XF) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
+    if constexpr (XF) {
         // 8 lanes per 32-value group, nh / 8 groups per pass; the loads of
         // up to 8 passes are issued before any is used (a load issued
         // behind the tile copies returns only when they have landed, so one
@@ -74,13 +76,13 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
             }
         }
     }
-    if (xf) {
+    if constexpr (XF) {
         xq = (const int8_t *)(tile + ((R * rb + 15u) & ~15u));
         xd = (const float *)(xq + (size_t)NT * K);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (xf) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
+    if constexpr (XF) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
     for (uint32_t rr = tid / TPR; rr < nr; rr += 256 / TPR) {
         float acc[NT];
 #pragma unroll
@@ -117,8 +119,14 @@ static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const fl
     const dim3 grid((rows + R - 1) / R), blk(256);
 #define Q4MI_L(T, P)                                                                     \
     if (L.tpr == T && L.gpt == P) {                                                      \
-        mmvq_k<F, NT, T, P><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, xq, xd, nt, \
-                                                          y, scale, sums);               \
+        if (xf)                                                                          \
+            mmvq_k<F, NT, T, P, true><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, \
+                                                                    xq, xd, nt, y, scale, \
+                                                                    sums);               \
+        else                                                                             \
+            mmvq_k<F, NT, T, P, false><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, \
+                                                                     xq, xd, nt, y, scale, \
+                                                                     sums);              \
         return launch_ok("mmvq_k");                                                      \
     }
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
