@@ -121,7 +121,10 @@ bool q4_hip_moe_exec_dev(const uint8_t *base, uint64_t stride, const int32_t *d_
  * t*64 + d_nh[t]); experts picked by several tokens are read once.  x, y
  * token-major.  Replaces q4_hip_moe_win_ok / q4_hip_moe_exec_win
  * (src/q4.h:906-913, src/q4_rocm.cu:7369-7531); covers every IQ3_S/Q8_0
- * layer (the reference required an IQ4_NL/Q2_0 down). */
+ * layer (the reference required an IQ4_NL/Q2_0 down).  Gate/up types: IQ3_S,
+ * Q8_0 and the reference window's IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_XS;
+ * down: IQ3_S, Q8_0, IQ4_NL, Q2_0, IQ2_S.  At most 64 (token, pick) entries
+ * per call: entries past the 64th are not read. */
 bool q4_hip_moe_win_ok(uint32_t gt, uint32_t ut, uint32_t dt, uint32_t in_dim, uint32_t n_ff,
                        uint32_t n_tok);
 bool q4_hip_moe_exec_win(const uint8_t *base, uint64_t stride, const int32_t *d_es,

@@ -16,9 +16,13 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 T_Q8_0 = 8
 T_Q6_K = 14
+T_IQ2_XXS = 16
+T_IQ2_XS = 17
+T_IQ3_XXS = 18
 T_IQ4_NL = 20
 T_IQ3_S = 21
 T_IQ2_S = 22
+T_IQ4_XS = 23
 T_Q2_0 = 42
 
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -33,7 +37,8 @@ def _p(a, t):
 
 
 _BLOCK = {T_IQ3_S: (256, 110), T_Q8_0: (32, 34), T_IQ4_NL: (32, 18), T_Q2_0: (64, 18),
-          T_IQ2_S: (256, 82), T_Q6_K: (256, 210)}
+          T_IQ2_S: (256, 82), T_Q6_K: (256, 210), T_IQ2_XXS: (256, 66), T_IQ2_XS: (256, 74),
+          T_IQ3_XXS: (256, 98), T_IQ4_XS: (256, 136)}
 
 
 def row_bytes(ty, n):

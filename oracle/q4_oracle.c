@@ -37,9 +37,14 @@
 
 #include "../include/q4mi_iq2s_grid.h"
 #include "../include/q4mi_iq3s_grid.h"
+#include "../include/q4mi_iqxx_grids.h"
 
 #define OR_T_Q8_0 8u
 #define OR_T_Q6_K 14u
+#define OR_T_IQ2_XXS 16u
+#define OR_T_IQ2_XS 17u
+#define OR_T_IQ3_XXS 18u
+#define OR_T_IQ4_XS 23u
 #define OR_T_IQ4_NL 20u
 #define OR_T_IQ3_S 21u
 #define OR_T_IQ2_S 22u
@@ -84,6 +89,10 @@ uint64_t or_row_bytes(uint32_t type, uint64_t n) {
     case OR_T_Q2_0: return n % 64 ? 0 : n / 64 * 18;
     case OR_T_IQ2_S: return n % 256 ? 0 : n / 256 * 82;
     case OR_T_Q6_K: return n % 256 ? 0 : n / 256 * 210;
+    case OR_T_IQ2_XXS: return n % 256 ? 0 : n / 256 * 66;
+    case OR_T_IQ2_XS: return n % 256 ? 0 : n / 256 * 74;
+    case OR_T_IQ3_XXS: return n % 256 ? 0 : n / 256 * 98;
+    case OR_T_IQ4_XS: return n % 256 ? 0 : n / 256 * 136;
     }
     return 0;
 }
@@ -96,10 +105,13 @@ static float or_h2f_at(const uint8_t *p) {
 
 /* Integers of one 32-value group of the non-IQ3_S formats: wi = the signed
  * integer weights, lm[l] = the integer multiplier of values 4l..4l+3, *d =
- * the float block scale (IQ2_S: d * 0.125).  Follows the reference's
- * dequantizers (src/q4_quant.c: Q2_0 :177-188, IQ4_NL :273-288, IQ2_S
- * :290-322, Q6_K :481-510), whose float value of element i is
- * *d * lm[i/4] * wi[i]. */
+ * the float block scale (IQ2_S, IQ2_XXS, IQ2_XS: d * 0.125; IQ3_XXS:
+ * d * 0.25).  Follows the reference's dequantizers (src/q4_quant.c: Q2_0
+ * :177-188, IQ4_NL :273-288, IQ2_S :290-322, IQ2_XS :324-347, IQ2_XXS
+ * :356-381, IQ3_XXS :424-453, IQ4_XS :455-477, Q6_K :481-510) and the
+ * integer structure of the CPU dots (src/q4_cpuexp.c: dq8_iq2_xs :740-772,
+ * dq8_iq2_xxs :777-810, dq8_iq3_xxs :895-935, dq8_iq4_xs :945-975): the value
+ * of element i is *d * lm[i/4] * wi[i]. */
 static void or_group_other(uint32_t type, const uint8_t *w, uint64_t g, int32_t wi[32],
                            int32_t lm[8], float *d) {
     for (int l = 0; l < 8; l++) lm[l] = 1;
@@ -129,6 +141,76 @@ static void or_group_other(uint32_t type, const uint8_t *w, uint64_t g, int32_t 
             }
         }
         for (int l = 0; l < 8; l++) lm[l] = 2 * (int32_t)(l < 4 ? (sc & 15) : (sc >> 4)) + 1;
+    } else if (type == OR_T_IQ2_XXS) {
+        /* group ib: u32 of four grid bytes, u32 of four 7-bit sign indexes
+         * and the 4-bit scale in its top nibble; multiplier 2*sc+1 */
+        const uint8_t *blk = w + 66 * (g / 8);
+        const int ib = (int)(g % 8);
+        *d = or_h2f_at(blk) * 0.125f;
+        const uint8_t *gb = blk + 2 + 8 * ib;
+        uint32_t aux;
+        memcpy(&aux, blk + 6 + 8 * ib, 4);
+        for (int l = 0; l < 4; l++) {
+            const uint64_t e = q4mi_iq2_decode(q4mi_iq2xxs_code[gb[l]]);
+            const uint32_t sg = q4mi_iq_sign_byte((aux >> (7 * l)) & 127u);
+            for (int j = 0; j < 8; j++) {
+                const int mag = (int)((e >> (8 * j)) & 0xff);
+                wi[8 * l + j] = ((sg >> j) & 1) ? -mag : mag;
+            }
+        }
+        for (int l = 0; l < 8; l++) lm[l] = 2 * (int32_t)(aux >> 28) + 1;
+    } else if (type == OR_T_IQ2_XS) {
+        /* group ib: four u16 = 9-bit grid index | 7-bit sign index << 9;
+         * scale byte ib: low nibble for values 0-15, high for 16-31 */
+        const uint8_t *blk = w + 74 * (g / 8);
+        const int ib = (int)(g % 8);
+        *d = or_h2f_at(blk) * 0.125f;
+        const uint32_t sc = blk[66 + ib];
+        for (int l = 0; l < 4; l++) {
+            uint16_t v;
+            memcpy(&v, blk + 2 + 8 * ib + 2 * l, 2);
+            const uint64_t e = q4mi_iq2_decode(q4mi_iq2xs_code[v & 511]);
+            const uint32_t sg = q4mi_iq_sign_byte(v >> 9);
+            for (int j = 0; j < 8; j++) {
+                const int mag = (int)((e >> (8 * j)) & 0xff);
+                wi[8 * l + j] = ((sg >> j) & 1) ? -mag : mag;
+            }
+        }
+        for (int l = 0; l < 8; l++) lm[l] = 2 * (int32_t)(l < 4 ? (sc & 15) : (sc >> 4)) + 1;
+    } else if (type == OR_T_IQ3_XXS) {
+        /* group ib: eight grid bytes (four values each) at 2 + 8ib; u32 at
+         * 66 + 4ib: four 7-bit sign indexes (eight values each), scale in
+         * the top nibble; value dl = d * (0.5 + sc) * 0.5 = d/4 * (2sc+1) */
+        const uint8_t *blk = w + 98 * (g / 8);
+        const int ib = (int)(g % 8);
+        *d = or_h2f_at(blk) * 0.25f;
+        const uint8_t *gb = blk + 2 + 8 * ib;
+        uint32_t aux;
+        memcpy(&aux, blk + 66 + 4 * ib, 4);
+        for (int k = 0; k < 8; k++) {
+            const uint32_t e = q4mi_iq3xxs_decode(q4mi_iq3xxs_code[gb[k]]);
+            const uint32_t sg = q4mi_iq_sign_byte((aux >> (7 * (k / 2))) & 127u);
+            for (int j = 0; j < 4; j++) {
+                const int mag = (int)((e >> (8 * j)) & 0xff);
+                wi[4 * k + j] = ((sg >> (4 * (k & 1) + j)) & 1) ? -mag : mag;
+            }
+        }
+        for (int l = 0; l < 8; l++) lm[l] = 2 * (int32_t)(aux >> 28) + 1;
+    } else if (type == OR_T_IQ4_XS) {
+        /* group ib: 6-bit scale ls (low 4 bits from scales_l, high 2 from
+         * scales_h), multiplier ls - 32; nibbles as IQ4_NL's */
+        const uint8_t *blk = w + 136 * (g / 8);
+        const int ib = (int)(g % 8);
+        *d = or_h2f_at(blk);
+        uint16_t sh;
+        memcpy(&sh, blk + 2, 2);
+        const int ls = ((blk[4 + ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+        const uint8_t *qs = blk + 8 + 16 * ib;
+        for (int j = 0; j < 16; j++) {
+            wi[j] = or_kv_iq4nl[qs[j] & 15];
+            wi[j + 16] = or_kv_iq4nl[qs[j] >> 4];
+        }
+        for (int l = 0; l < 8; l++) lm[l] = ls - 32;
     } else { /* Q6_K: group g = 32 values of a 256-value superblock */
         const uint8_t *blk = w + 210 * (g / 8);
         const int j = (int)(g % 8), h = j / 4, gq = j % 4;
@@ -203,6 +285,14 @@ int or_dequant_row(uint32_t type, const uint8_t *w, uint64_t n, float *y) {
                 if (type == OR_T_IQ2_S)   /* dl = d * (0.5 + s) * 0.25 */
                     v = (or_h2f_at(w + 82 * (g / 8)) * (0.5f + (float)((lm[i / 4] - 1) / 2)) *
                          0.25f) * (float)wi[i];
+                else if (type == OR_T_IQ2_XXS || type == OR_T_IQ2_XS)
+                    /* dl = d * 0.125 * (2s+1); value = dl * mag * sign */
+                    v = (d * (float)lm[i / 4]) * (float)wi[i];
+                else if (type == OR_T_IQ3_XXS) /* db = d * (0.5 + s) * 0.5 */
+                    v = (or_h2f_at(w + 98 * (g / 8)) * (0.5f + (float)((lm[i / 4] - 1) / 2)) *
+                         0.5f) * (float)wi[i];
+                else if (type == OR_T_IQ4_XS) /* dl = d * (ls - 32) */
+                    v = (d * (float)lm[i / 4]) * (float)wi[i];
                 else if (type == OR_T_Q6_K) /* d * sc * (q - 32) */
                     v = d * (float)lm[i / 4] * (float)wi[i];
                 else
@@ -272,7 +362,9 @@ static void or_group_ints(uint32_t type, const uint8_t *w, uint64_t g,
 }
 
 static int or_other(uint32_t type) {
-    return type == OR_T_IQ4_NL || type == OR_T_Q2_0 || type == OR_T_IQ2_S || type == OR_T_Q6_K;
+    return type == OR_T_IQ4_NL || type == OR_T_Q2_0 || type == OR_T_IQ2_S || type == OR_T_Q6_K ||
+           type == OR_T_IQ2_XXS || type == OR_T_IQ2_XS || type == OR_T_IQ3_XXS ||
+           type == OR_T_IQ4_XS;
 }
 
 /* Exact per-group sums S_g = sum_l lm_l * sum_{i in quad l} w_i q_i (int32;
@@ -308,7 +400,9 @@ float or_dot8(uint32_t type, const uint8_t *w, uint64_t n, const int8_t *q,
     int32_t wi[32], mult, lm[8];
     if (or_other(type)) {
         /* IQ4_NL, IQ2_S (dq8_iq4_nl / dq8_iq2_s, src/q4_cpuexp.c:814-853,
-         * :978-1005): lane l gets fma(d*d_x, lm_l * sum of quad l, .);
+         * :978-1005), and IQ2_XS, IQ2_XXS, IQ3_XXS, IQ4_XS (:740-772,
+         * :777-810, :895-935, :945-975): lane l gets
+         * fma(d*d_x, lm_l * sum of quad l, .);
          * Q2_0 (dq8_q2_0 :1113-1150): lanes take the unsigned codes
          * (w + 1) and a serial cs = fma(d*d_x, sum(q), cs) is subtracted after the
          * fold.  Q6_K (no CPU expert kernel in the reference) uses the

@@ -103,6 +103,9 @@ int qref_dot8_rows(uint32_t type, const uint8_t *w, uint64_t rows, uint64_t n,
     const uint64_t rb = q4_row_bytes(type, n);
     if (!rb) return 0;
     const uint64_t ng = n / 32;
+    /* the sign-expansion table the IQ2/IQ3_XXS kernels read, set up by the
+     * reference's dispatchers before their first dot (src/q4_cpuexp.c:2595) */
+    cpx_esigns_init();
     cpx_q8 *xq = (cpx_q8 *)malloc(nt * ng * sizeof(cpx_q8));
     if (!xq) return 0;
     for (uint32_t t = 0; t < nt; t++) cpx_quant8(x + t * n, n, xq + t * ng);

@@ -16,6 +16,21 @@
 //                       grid[qs[4ib+l] | ((qh[ib] << (8-2l)) & 0x300)], sign
 //                       bit j of signs[4ib+l] negates value j; multiplier
 //                       2*nibble+1 (low nibble: values 0-15), d * 0.125
+//   IQ2_XXS 66 B / 256: d | per group ib a u32 of four grid bytes (8
+//                       values each, {8, 25, 43}) and a u32 of four 7-bit
+//                       sign indexes (bit 7 of the sign byte = parity) and
+//                       the 4-bit scale s in its top nibble; multiplier
+//                       2s+1, d * 0.125
+//   IQ2_XS  74 B / 256: d | qs[32] u16 = 9-bit grid index | 7-bit sign
+//                       index << 9 | scales[8]: low nibble values 0-15,
+//                       high 16-31, multipliers 2*nibble+1, d * 0.125
+//   IQ3_XXS 98 B / 256: d | qs[64] grid bytes (4 values each, {4 .. 62}) |
+//                       per group a u32 of four 7-bit sign indexes (8 values
+//                       each) and the scale s in its top nibble; multiplier
+//                       2s+1, d * 0.25
+//   IQ4_XS 136 B / 256: d | scales_h u16 | scales_l[4] | qs[128]: group ib
+//                       as IQ4_NL's nibbles at qs[16 ib], multiplier
+//                       ls - 32, ls = 4 bits of scales_l | 2 of scales_h
 //   Q6_K   210 B / 256: ql[128] | qh[64] | int8 sc[16] | d: half h (128
 //                       values), group gq = 0..3 of it, value l = (4-bit
 //                       from ql[64h + 32(gq&1) + l] (high nibble when gq&2)
@@ -24,8 +39,13 @@
 #pragma once
 #include "q4mi_common.h"
 #include "../../include/q4mi_iq2s_grid.h"
+#include "../../include/q4mi_iqxx_grids.h"
 
 #define Q4MI_T_Q6_K 14u
+#define Q4MI_T_IQ2_XXS 16u
+#define Q4MI_T_IQ2_XS 17u
+#define Q4MI_T_IQ3_XXS 18u
+#define Q4MI_T_IQ4_XS 23u
 #define Q4MI_T_IQ4_NL 20u
 #define Q4MI_T_IQ2_S 22u
 #define Q4MI_T_Q2_0 42u
@@ -39,6 +59,9 @@ struct WGroup {
 };
 
 __constant__ uint16_t q4mi_iq2s_code_dev[1024] = {Q4MI_IQ2S_CODES};
+__constant__ uint16_t q4mi_iq2xxs_code_dev[256] = {Q4MI_IQ2XXS_CODES};
+__constant__ uint16_t q4mi_iq2xs_code_dev[512] = {Q4MI_IQ2XS_CODES};
+__constant__ uint16_t q4mi_iq3xxs_code_dev[256] = {Q4MI_IQ3XXS_CODES};
 
 // Four consecutive dwords (any 2-byte-aligned LDS byte offset) as u32.
 __device__ inline void lds_dwords(const uint32_t *lw, uint32_t off, uint32_t (&o)[4]) {
@@ -202,6 +225,155 @@ struct FmtQ6K {
     }
 };
 
+
+// ------------------------------------------- IQ2_XXS, IQ2_XS, IQ3_XXS
+// LDS: the grid as magnitude dwords and the 7-bit sign index -> two byte-mask
+// dwords table (the sign byte's bit 7 is the parity of the other seven).
+__device__ inline uint2 iqxx_sign_masks(uint32_t i) {
+    const uint32_t sb = i | ((__popc(i) & 1u) << 7);
+    return make_uint2(q4mi_expand4(sb & 15u), q4mi_expand4(sb >> 4));
+}
+__device__ inline uint32_t iq2_level_dev(uint32_t c) { return c == 0 ? 8u : c == 1 ? 25u : 43u; }
+
+template <uint32_t N>
+struct Iq2xLds {
+    uint2 grid[N];
+    uint2 smask[128];
+};
+
+template <uint32_t N>
+__device__ inline void iq2x_init(Iq2xLds<N> *t, const uint16_t *codes, uint32_t tid, uint32_t n) {
+    for (uint32_t i = tid; i < N; i += n) {
+        const uint32_t c = codes[i];
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            lo |= iq2_level_dev((c >> (2 * j)) & 3u) << (8 * j);
+            hi |= iq2_level_dev((c >> (2 * j + 8)) & 3u) << (8 * j);
+        }
+        t->grid[i] = make_uint2(lo, hi);
+    }
+    for (uint32_t i = tid; i < 128; i += n) t->smask[i] = iqxx_sign_masks(i);
+}
+
+struct FmtIQ2XXS {
+    static constexpr uint32_t kType = Q4MI_T_IQ2_XXS;
+    static constexpr uint32_t kTabBytes = sizeof(Iq2xLds<256>);
+    static constexpr bool kTwo = false;
+    __device__ static inline void init(void *tab, uint32_t tid, uint32_t n) {
+        iq2x_init((Iq2xLds<256> *)tab, q4mi_iq2xxs_code_dev, tid, n);
+    }
+    __device__ static inline void decode(const void *tab, const uint8_t *lb, const uint32_t *lw,
+                                         uint32_t row, uint32_t g, WGroup &o) {
+        const Iq2xLds<256> *t = (const Iq2xLds<256> *)tab;
+        const uint32_t B = row + 66u * (g >> 3), ib = g & 7u;
+        o.d = q4mi_h2f(lds_u16_at(lb, B)) * 0.125f;
+        const uint32_t gi = lds_u32_at(lw, B + 2u + 8u * ib);
+        const uint32_t aux = lds_u32_at(lw, B + 6u + 8u * ib);
+        o.m1 = o.m2 = 2 * (int)(aux >> 28) + 1;
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint2 e = t->grid[(gi >> (8 * l)) & 0xffu];
+            const uint2 m = t->smask[(aux >> (7 * l)) & 127u];
+            o.w[2 * l] = q4mi_sign4(e.x, m.x);
+            o.w[2 * l + 1] = q4mi_sign4(e.y, m.y);
+        }
+    }
+};
+
+struct FmtIQ2XS {
+    static constexpr uint32_t kType = Q4MI_T_IQ2_XS;
+    static constexpr uint32_t kTabBytes = sizeof(Iq2xLds<512>);
+    static constexpr bool kTwo = true;
+    __device__ static inline void init(void *tab, uint32_t tid, uint32_t n) {
+        iq2x_init((Iq2xLds<512> *)tab, q4mi_iq2xs_code_dev, tid, n);
+    }
+    __device__ static inline void decode(const void *tab, const uint8_t *lb, const uint32_t *lw,
+                                         uint32_t row, uint32_t g, WGroup &o) {
+        const Iq2xLds<512> *t = (const Iq2xLds<512> *)tab;
+        const uint32_t B = row + 74u * (g >> 3), ib = g & 7u;
+        o.d = q4mi_h2f(lds_u16_at(lb, B)) * 0.125f;
+        const uint32_t v01 = lds_u32_at(lw, B + 2u + 8u * ib);
+        const uint32_t v23 = lds_u32_at(lw, B + 6u + 8u * ib);
+        const uint32_t sc = lds_u8_at(lb, B + 66u + ib);
+        o.m1 = 2 * (int)(sc & 15u) + 1;
+        o.m2 = 2 * (int)(sc >> 4) + 1;
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const uint32_t v = ((l < 2 ? v01 : v23) >> (16 * (l & 1))) & 0xffffu;
+            const uint2 e = t->grid[v & 511u];
+            const uint2 m = t->smask[v >> 9];
+            o.w[2 * l] = q4mi_sign4(e.x, m.x);
+            o.w[2 * l + 1] = q4mi_sign4(e.y, m.y);
+        }
+    }
+};
+
+struct Iq3xxsLds {
+    uint32_t grid[256];
+    uint2 smask[128];
+};
+
+struct FmtIQ3XXS {
+    static constexpr uint32_t kType = Q4MI_T_IQ3_XXS;
+    static constexpr uint32_t kTabBytes = sizeof(Iq3xxsLds);
+    static constexpr bool kTwo = false;
+    __device__ static inline void init(void *tab, uint32_t tid, uint32_t n) {
+        Iq3xxsLds *t = (Iq3xxsLds *)tab;
+        for (uint32_t i = tid; i < 256; i += n) {
+            const uint32_t c = q4mi_iq3xxs_code_dev[i];
+            uint32_t v = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t k = (c >> (3 * j)) & 7u;
+                v |= (k == 7u ? 62u : 8u * k + 4u) << (8 * j);
+            }
+            t->grid[i] = v;
+        }
+        for (uint32_t i = tid; i < 128; i += n) t->smask[i] = iqxx_sign_masks(i);
+    }
+    __device__ static inline void decode(const void *tab, const uint8_t *lb, const uint32_t *lw,
+                                         uint32_t row, uint32_t g, WGroup &o) {
+        const Iq3xxsLds *t = (const Iq3xxsLds *)tab;
+        const uint32_t B = row + 98u * (g >> 3), ib = g & 7u;
+        o.d = q4mi_h2f(lds_u16_at(lb, B)) * 0.25f;
+        const uint32_t q0 = lds_u32_at(lw, B + 2u + 8u * ib);
+        const uint32_t q1 = lds_u32_at(lw, B + 6u + 8u * ib);
+        const uint32_t aux = lds_u32_at(lw, B + 66u + 4u * ib);
+        o.m1 = o.m2 = 2 * (int)(aux >> 28) + 1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t gb = ((k < 4 ? q0 : q1) >> (8 * (k & 3))) & 0xffu;
+            const uint2 m = t->smask[(aux >> (7 * (k >> 1))) & 127u];
+            o.w[k] = q4mi_sign4(t->grid[gb], (k & 1) ? m.y : m.x);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ IQ4_XS
+struct FmtIQ4XS {
+    static constexpr uint32_t kType = Q4MI_T_IQ4_XS;
+    static constexpr uint32_t kTabBytes = 0;
+    static constexpr bool kTwo = false;
+    __device__ static inline void init(void *, uint32_t, uint32_t) {}
+    __device__ static inline void decode(const void *, const uint8_t *lb, const uint32_t *lw,
+                                         uint32_t row, uint32_t g, WGroup &o) {
+        const uint32_t B = row + 136u * (g >> 3), ib = g & 7u;
+        o.d = q4mi_h2f(lds_u16_at(lb, B));
+        const uint32_t sh = lds_u16_at(lb, B + 2u);
+        const uint32_t sl = lds_u8_at(lb, B + 4u + (ib >> 1));
+        const int ls = (int)(((sl >> (4 * (ib & 1u))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+        o.m1 = o.m2 = ls - 32;
+        uint32_t q[4];
+        lds_dwords(lw, B + 8u + 16u * ib, q);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o.w[k] = iq4nl_map(q[k] & 0x0F0F0F0Fu);
+            o.w[k + 4] = iq4nl_map((q[k] >> 4) & 0x0F0F0F0Fu);
+        }
+    }
+};
+
 template <uint32_t TY>
 struct FmtOf;
 template <>
@@ -219,6 +391,22 @@ struct FmtOf<Q4MI_T_IQ2_S> {
 template <>
 struct FmtOf<Q4MI_T_Q6_K> {
     using F = FmtQ6K;
+};
+template <>
+struct FmtOf<Q4MI_T_IQ2_XXS> {
+    using F = FmtIQ2XXS;
+};
+template <>
+struct FmtOf<Q4MI_T_IQ2_XS> {
+    using F = FmtIQ2XS;
+};
+template <>
+struct FmtOf<Q4MI_T_IQ3_XXS> {
+    using F = FmtIQ3XXS;
+};
+template <>
+struct FmtOf<Q4MI_T_IQ4_XS> {
+    using F = FmtIQ4XS;
 };
 
 }  // namespace q4mi

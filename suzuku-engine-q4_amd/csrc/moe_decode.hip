@@ -26,13 +26,18 @@ static bool run_nt(uint32_t ty_gu, uint32_t ty_dn, const MoeArgs &a, uint32_t nu
 }
 
 // Rows are staged with 4- or 16-byte copies, so a row's byte size must be a
-// multiple of 4 (IQ3_S: K a multiple of 512; Q8_0, IQ4_NL, Q2_0: of 64;
-// IQ2_S: of 512).  Gate/up: IQ3_S, Q8_0, IQ2_S; down also IQ4_NL, Q2_0.
+// multiple of 4 (IQ3_S, IQ2_S, IQ2_XXS, IQ2_XS, IQ3_XXS: K a multiple of
+// 512; Q8_0, IQ4_NL, Q2_0: of 64; IQ4_XS: of 256).  Gate/up: IQ3_S, Q8_0,
+// IQ2_S, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ4_XS; down: IQ3_S, Q8_0, IQ2_S, IQ4_NL,
+// Q2_0.
 static bool type_ok(uint32_t ty, uint32_t K, bool down) {
     switch (ty) {
     case Q4MI_T_IQ3_S: case Q4MI_T_Q8_0: case Q4MI_T_IQ2_S: break;
     case Q4MI_T_IQ4_NL: case Q4MI_T_Q2_0:
         if (!down) return false;
+        break;
+    case Q4MI_T_IQ2_XXS: case Q4MI_T_IQ2_XS: case Q4MI_T_IQ3_XXS: case Q4MI_T_IQ4_XS:
+        if (down) return false;
         break;
     default: return false;
     }

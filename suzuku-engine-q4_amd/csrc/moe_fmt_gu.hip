@@ -1,16 +1,27 @@
 // Gate/up kernels of the decode / verify window for the weight formats of
-// formats.h (IQ2_S), in their own translation unit so the library's
+// formats.h (IQ2_S, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ4_XS), in their own translation unit so the library's
 // kernels compile in parallel.
 #include "moe_kern.h"
 
 namespace q4mi {
 
+template <uint32_t TY>
+static bool gu_nt(int nt, const MoeArgs &a, uint32_t nu_host) {
+    if (nt == 1) return gu_dispatch<TY, 1>(a, nu_host);
+    if (nt == 2) return gu_dispatch<TY, 2>(a, nu_host);
+    if (nt <= 4) return gu_dispatch<TY, 4>(a, nu_host);
+    return gu_dispatch<TY, 8>(a, nu_host);
+}
+
+// the reference window's other gate/up formats (win_iq_bb,
+// src/q4_rocm.cu:7333-7343): IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_XS
 bool moe_fmt_gu(uint32_t ty, int nt, const MoeArgs &a, uint32_t nu_host) {
-    if (ty == Q4MI_T_IQ2_S) {
-        if (nt == 1) return gu_dispatch<Q4MI_T_IQ2_S, 1>(a, nu_host);
-        if (nt == 2) return gu_dispatch<Q4MI_T_IQ2_S, 2>(a, nu_host);
-        if (nt <= 4) return gu_dispatch<Q4MI_T_IQ2_S, 4>(a, nu_host);
-        return gu_dispatch<Q4MI_T_IQ2_S, 8>(a, nu_host);
+    switch (ty) {
+    case Q4MI_T_IQ2_S: return gu_nt<Q4MI_T_IQ2_S>(nt, a, nu_host);
+    case Q4MI_T_IQ2_XXS: return gu_nt<Q4MI_T_IQ2_XXS>(nt, a, nu_host);
+    case Q4MI_T_IQ2_XS: return gu_nt<Q4MI_T_IQ2_XS>(nt, a, nu_host);
+    case Q4MI_T_IQ3_XXS: return gu_nt<Q4MI_T_IQ3_XXS>(nt, a, nu_host);
+    case Q4MI_T_IQ4_XS: return gu_nt<Q4MI_T_IQ4_XS>(nt, a, nu_host);
     }
     set_error("moe: gate/up type %u not covered", ty);
     return false;

@@ -329,11 +329,13 @@ __device__ inline void q80_group(const uint8_t *lb, const uint32_t *lw, uint32_t
 // LDS table bytes of a format's decoder (at the start of the kernel's LDS).
 template <uint32_t TY>
 __host__ __device__ constexpr uint32_t tab_bytes() {
-    return TY == Q4MI_T_IQ3_S ? 32768u : TY == Q4MI_T_IQ2_S ? (uint32_t)sizeof(Iq2sLds) : 0u;
+    if constexpr (TY == Q4MI_T_IQ3_S) return 32768u;
+    else if constexpr (TY == Q4MI_T_Q8_0) return 0u;
+    else return (uint32_t)FmtOf<TY>::F::kTabBytes;
 }
 template <uint32_t TY>
 __host__ __device__ constexpr bool two_mult() {
-    return TY == Q4MI_T_IQ2_S;
+    return TY == Q4MI_T_IQ2_S || TY == Q4MI_T_IQ2_XS;
 }
 
 // One 32-value group: signed quads, the multipliers of quads 0-3 / 4-7 and
@@ -1125,8 +1127,11 @@ size_t lds_cap();
 constexpr size_t kPlanTable = 4096;
 
 static size_t head_bytes(uint32_t ty) {
-    const size_t tab = ty == Q4MI_T_IQ3_S ? tab_bytes<Q4MI_T_IQ3_S>()
-                     : ty == Q4MI_T_IQ2_S ? tab_bytes<Q4MI_T_IQ2_S>() : 0;
+    const size_t tab = ty == Q4MI_T_IQ3_S   ? tab_bytes<Q4MI_T_IQ3_S>()
+                     : ty == Q4MI_T_IQ2_S   ? tab_bytes<Q4MI_T_IQ2_S>()
+                     : ty == Q4MI_T_IQ2_XXS ? tab_bytes<Q4MI_T_IQ2_XXS>()
+                     : ty == Q4MI_T_IQ2_XS  ? tab_bytes<Q4MI_T_IQ2_XS>()
+                     : ty == Q4MI_T_IQ3_XXS ? tab_bytes<Q4MI_T_IQ3_XXS>() : 0;
     return al16(tab + sizeof(Plan) + sizeof(Sync));
 }
 

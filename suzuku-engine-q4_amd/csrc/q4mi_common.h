@@ -31,6 +31,10 @@ __host__ __device__ inline uint64_t q4mi_row_bytes(uint32_t ty, uint64_t n) {
     case 20u: return n % 32 ? 0 : n / 32 * 18;      // IQ4_NL
     case 22u: return n % 256 ? 0 : n / 256 * 82;    // IQ2_S
     case 42u: return n % 64 ? 0 : n / 64 * 18;      // Q2_0
+    case 16u: return n % 256 ? 0 : n / 256 * 66;    // IQ2_XXS
+    case 17u: return n % 256 ? 0 : n / 256 * 74;    // IQ2_XS
+    case 18u: return n % 256 ? 0 : n / 256 * 98;    // IQ3_XXS
+    case 23u: return n % 256 ? 0 : n / 256 * 136;   // IQ4_XS
     }
     return 0;
 }
@@ -138,7 +142,8 @@ __device__ inline uint32_t lds_u16_at(const uint8_t *b, uint32_t off) {
 }
 
 // Signed int8 weights of grid entry gv under a byte mask m (0xff = negate):
-// (g ^ m) + (m & 1) per byte; magnitudes are 1..15 so no byte carries out.
+// (g ^ m) + (m & 1) per byte; magnitudes are nonzero and below 128 (1..62
+// in the IQ grids), so no byte carries out.
 __device__ inline int32_t q4mi_sign4(uint32_t gv, uint32_t m) {
     return (int32_t)((gv ^ m) + (m & 0x01010101u));
 }

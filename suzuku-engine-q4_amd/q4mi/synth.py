@@ -33,9 +33,12 @@ def q80_bytes(rng, nblocks):
 
 
 T_Q6_K, T_IQ4_NL, T_IQ2_S, T_Q2_0 = 14, 20, 22, 42
+T_IQ2_XXS, T_IQ2_XS, T_IQ3_XXS, T_IQ4_XS = 16, 17, 18, 23
 # (values per block, bytes per block, offset of the fp16 scale)
 BLOCKS = {T_IQ3_S: (256, 110, 0), T_Q8_0: (32, 34, 0), T_IQ4_NL: (32, 18, 0),
-          T_Q2_0: (64, 18, 0), T_IQ2_S: (256, 82, 0), T_Q6_K: (256, 210, 208)}
+          T_Q2_0: (64, 18, 0), T_IQ2_S: (256, 82, 0), T_Q6_K: (256, 210, 208),
+          T_IQ2_XXS: (256, 66, 0), T_IQ2_XS: (256, 74, 0), T_IQ3_XXS: (256, 98, 0),
+          T_IQ4_XS: (256, 136, 0)}
 
 
 def blocks_bytes(rng, ty, nblocks):

@@ -1,5 +1,6 @@
 """GPU parity for the weight formats beside IQ3_S / Q8_0 (IQ4_NL, Q2_0,
-IQ2_S, Q6_K), through the C ABI, against the C oracle (whose decoders and
+IQ2_S, Q6_K; IQ2_XXS, IQ2_XS, IQ3_XXS, IQ4_XS as decode / window gate/up),
+through the C ABI, against the C oracle (whose decoders and
 int8 dots are pinned bit for bit against the reference's CPU code in
 tests/test_oracle_formats.py).
 
@@ -18,6 +19,8 @@ from q4mi import synth
 pytestmark = pytest.mark.gpu
 T_IQ3_S, T_Q8_0 = q4mi.T_IQ3_S, q4mi.T_Q8_0
 T_Q6_K, T_IQ4_NL, T_IQ2_S, T_Q2_0 = 14, 20, 22, 42
+T_IQ2_XXS, T_IQ2_XS, T_IQ3_XXS, T_IQ4_XS = 16, 17, 18, 23
+IQXX = [T_IQ2_XXS, T_IQ2_XS, T_IQ3_XXS, T_IQ4_XS]
 TOL = 1e-3
 
 
@@ -130,12 +133,93 @@ def test_moe_layer_formats(gpu, oracle, tg, td, n_tok):
     assert rel_err(host(y), yo) <= TOL
 
 
+def h_tie_margin(h):
+    """Smallest distance of h*127/amax (per 32-value group) from a q8
+    rounding boundary."""
+    g = np.asarray(h, np.float64).reshape(-1, 32)
+    v = g * 127.0 / np.maximum(np.abs(g).max(1, keepdims=True), 1e-30)
+    return float(np.abs(np.abs(v - np.floor(v)) - 0.5).min())
+
+
+def check_tokens(oracle, y, yo, h, ids, w, arena, stride, od, td, H, F):
+    """Per token: a token whose oracle h is at least 2e-5 from every q8
+    rounding tie must match to TOL; a token with h on a tie only to twice
+    the oracle's own shift under a 1e-7 relative perturbation of its h (the
+    decode tests' rule).  Returns the number of tokens on a tie."""
+    rd = om.row_bytes(td, F)
+    k = ids.shape[1]
+    ties = 0
+    for t in range(ids.shape[0]):
+        ht = h[t * k:(t + 1) * k]
+        if min(h_tie_margin(hj) for hj in ht) >= 2e-5:
+            assert rel_err(y[t], yo[t]) <= TOL, t
+            continue
+        ties += 1
+        pr = np.random.default_rng(1)
+        yp = np.zeros(H, np.float32)
+        for j, e in enumerate(ids[t]):
+            hj = (ht[j] * (1 + 1e-7 * pr.standard_normal(F))).astype(np.float32)
+            wd = arena[e * stride + od:e * stride + od + H * rd]
+            yp += w[t, j] * oracle.dot8_rows(td, wd, H, F, hj[None])[0]
+        assert rel_err(y[t], yo[t]) <= max(TOL, 2 * rel_err(yp, yo[t])), t
+    return ties
+
+
+@pytest.mark.parametrize("tg", IQXX)
+@pytest.mark.parametrize("td", [T_IQ4_NL, T_IQ3_S])
+@pytest.mark.parametrize("n_tok", [1, 4, 8])
+def test_moe_layer_iq_gate_up(gpu, oracle, tg, td, n_tok):
+    """The reference window's other gate/up formats (IQ2_XXS, IQ2_XS,
+    IQ3_XXS, IQ4_XS; win_iq_bb, src/q4_rocm.cu:7333-7343) through the decode
+    layer (1 token, host list) and the 2..8-token window, against the
+    oracle (whose window layer matches the reference's q4_cpuex_dispatch_win
+    for these formats), token by token with the q8(h) tie rule of
+    check_tokens."""
+    H, F, E = 2048, 512, 24
+    rng = np.random.default_rng(tg * 1000 + td * 10 + n_tok)
+    arena, stride, og, ou, od = packed_experts(rng, E, H, F, tg, td)
+    d_arena = dev(arena)
+    x = rng.standard_normal((n_tok, H)).astype(np.float32)
+    k = 9 if n_tok <= 4 else 7   # n_tok * k <= 64, the window's entry bound
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    yo, h = oracle.moe_tokens(H, F, tg, td, arena, stride, x, ids, w, want_h=True)
+    P = q4mi.ptr
+    if n_tok == 1:
+        y = dev(np.zeros(H, np.float32))
+        i0, w0 = np.ascontiguousarray(ids[0]), np.ascontiguousarray(w[0])
+        q4mi.check(gpu.q4_hip_moe_exec(P(d_arena), stride, i0.ctypes.data_as(ctypes.c_void_p),
+                                       w0.ctypes.data_as(ctypes.c_void_p), k, tg, og, tg, ou, td,
+                                       od, P(dev(x[0])), None, None, None, P(y), F, H, H),
+                   "q4_hip_moe_exec")
+        got = host(y)[None]
+    else:
+        es = np.full((n_tok, 64), -1, np.int32)
+        ew = np.zeros((n_tok, 64), np.float32)
+        es[:, :k], ew[:, :k] = ids, w
+        assert gpu.q4_hip_moe_win_ok(tg, tg, td, H, F, n_tok)
+        y = dev(np.zeros((n_tok, H), np.float32))
+        q4mi.check(gpu.q4_hip_moe_exec_win(P(d_arena), stride, P(dev(es)), P(dev(ew)),
+                                           P(dev(np.full(n_tok, k, np.int32))), n_tok, tg, og, tg,
+                                           ou, td, od, P(dev(x)), None, P(y), F, H, H), "exec_win")
+        got = host(y)
+    ties = check_tokens(oracle, got, yo, h, ids, w, arena, stride, od, td, H, F)
+    assert ties <= max(1, n_tok // 2)
+
+
 def test_format_coverage_rules(gpu):
     """IQ4_NL and Q2_0 are down-projection types here (gate/up rejected);
-    Q6_K is an LM-head type (not in the routed layer)."""
+    IQ2_XXS, IQ2_XS, IQ3_XXS and IQ4_XS gate/up types (down rejected), as in
+    the reference's window; Q6_K is an LM-head type (not in the routed
+    layer)."""
     assert gpu.q4_hip_moe_win_ok(T_IQ2_S, T_IQ2_S, T_Q2_0, 2048, 512, 4)
     assert not gpu.q4_hip_moe_win_ok(T_IQ4_NL, T_IQ4_NL, T_IQ3_S, 2048, 512, 4)
     assert not gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, T_Q6_K, 2048, 512, 4)
+    for t in IQXX:
+        assert gpu.q4_hip_moe_win_ok(t, t, T_IQ4_NL, 2048, 512, 4)
+        assert not gpu.q4_hip_moe_win_ok(T_IQ3_S, T_IQ3_S, t, 2048, 512, 4)
+    # IQ2_XXS rows must be whole dwords: 66 B per 256 values -> K % 512
+    assert not gpu.q4_hip_moe_win_ok(T_IQ2_XXS, T_IQ2_XXS, T_IQ4_NL, 256 * 3, 512, 4)
 
 
 def mmq_q8(L, x, rows_idx, K):

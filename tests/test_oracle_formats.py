@@ -1,7 +1,9 @@
-"""The oracle's other weight formats (IQ4_NL, Q2_0, IQ2_S, Q6_K) pinned
-against the reference's own code compiled from source (oracle/_ref):
-dequantization bit for bit against q4_dequant_row; the int8 row dot bit for
-bit against the CPU expert kernels (dq8_iq4_nl, dq8_q2_0, dq8_iq2_s); and
+"""The oracle's other weight formats (IQ4_NL, Q2_0, IQ2_S, Q6_K, IQ2_XXS,
+IQ2_XS, IQ3_XXS, IQ4_XS) pinned against the reference's own code compiled
+from source (oracle/_ref): dequantization bit for bit against
+q4_dequant_row; the int8 row dot bit for bit against the CPU expert kernels
+(dq8_iq4_nl, dq8_q2_0, dq8_iq2_s, dq8_iq2_xxs, dq8_iq2_xs, dq8_iq3_xxs,
+dq8_iq4_xs); and
 the exact integer group sums against the dequantized values (d * S_g equals
 sum_i v_i q_i in exact arithmetic)."""
 import numpy as np
@@ -10,8 +12,11 @@ import pytest
 import oracle as om
 from q4mi import synth
 
-FMTS = [om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S, om.T_Q6_K]
-CPU_Q8 = [om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S]   # types with a reference int8 CPU kernel
+IQXX = [om.T_IQ2_XXS, om.T_IQ2_XS, om.T_IQ3_XXS, om.T_IQ4_XS]
+FMTS = [om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S, om.T_Q6_K] + IQXX
+CPU_Q8 = [om.T_IQ4_NL, om.T_Q2_0, om.T_IQ2_S] + IQXX   # types with a reference int8 CPU kernel
+# the fp16 block scale's factor in the value (d * factor * multiplier * integer)
+DFAC = {om.T_IQ2_S: 0.125, om.T_IQ2_XXS: 0.125, om.T_IQ2_XS: 0.125, om.T_IQ3_XXS: 0.25}
 
 
 @pytest.mark.parametrize("ty", FMTS)
@@ -53,7 +58,7 @@ def test_group_sums_exact(oracle, ty):
         vals, nb, doff = synth.BLOCKS[ty]
         blk = row.reshape(-1, nb)
         dscale = blk[:, doff:doff + 2].copy().view(np.float16).astype(np.float64).ravel()
-        per_group = np.repeat(dscale, vals // 32) * (0.125 if ty == om.T_IQ2_S else 1.0)
+        per_group = np.repeat(dscale, vals // 32) * DFAC.get(ty, 1.0)
         exact = (v * q.astype(np.float64)).reshape(-1, 32).sum(1)
         got = per_group * s.astype(np.float64)
         if ty == om.T_Q6_K:   # fp32 value d*sc*(q-32) may round (25 bits)
@@ -73,3 +78,35 @@ def test_q2_0_zero_codes_and_known_values(oracle):
     assert np.all(oracle.dequant_row(om.T_Q2_0, b, 64) == 1.0)
     b[2:] = 0x00
     assert np.all(oracle.dequant_row(om.T_Q2_0, b, 64) == -0.5)
+
+
+def _arena(rng, E, H, F, tg, td):
+    g = synth.matrix(rng, tg, E * F, H)
+    u = synth.matrix(rng, tg, E * F, H)
+    d = synth.matrix(rng, td, E * H, F)
+    gs, ds = F * om.row_bytes(tg, H), H * om.row_bytes(td, F)
+    arena = np.concatenate([np.concatenate([g[e * gs:(e + 1) * gs], u[e * gs:(e + 1) * gs],
+                                            d[e * ds:(e + 1) * ds]]) for e in range(E)])
+    return arena, 2 * gs + ds
+
+
+@pytest.mark.parametrize("tg", IQXX)
+def test_moe_window_formats_vs_reference(oracle, ref, tg):
+    """The oracle's verify-window layer with IQ2_XXS / IQ2_XS / IQ3_XXS /
+    IQ4_XS gate/up (the reference window's gate/up formats, win_iq_bb
+    src/q4_rocm.cu:7333-7343) and IQ4_NL down against the reference's own
+    q4_cpuex_dispatch_win on the same arena."""
+    from conftest import rel_err
+    rng = np.random.default_rng(300 + tg)
+    H, F, E, T, k = 512, 256, 12, 4, 4
+    arena, stride = _arena(rng, E, H, F, tg, om.T_IQ4_NL)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = rng.random((T, k)).astype(np.float32)
+    yr = ref.moe_win(H, F, tg, om.T_IQ4_NL, E, arena, stride, x, ids, wts,
+                     np.full(T, k, np.uint32))
+    yo = oracle.moe_tokens(H, F, tg, om.T_IQ4_NL, arena, stride, x, ids, wts)
+    assert np.abs(yr).max() > 0
+    # (the reference's pool splits the layer's jobs over threads; a q8(h) code
+    # at a rounding boundary may differ, ~1e-5 of the output norm)
+    assert rel_err(yo, yr) < 1e-4
