@@ -381,6 +381,9 @@ def main():
     if not args.no_extra:
         out["config3_window"] = bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL,
                                              capture, timed, args)
+        if not args.profile and not args.no_extra:
+            out["window_reference_shapes"] = bench_window_mixes(L, torch, np, q4mi, synth,
+                                                                capture, timed, args)
         if not args.profile:
             out["config2_routed"] = bench_routed(L, torch, np, q4mi, arenas, stride, og, ou,
                                                  od, NL, capture, timed, args)
@@ -872,6 +875,81 @@ def bench_window(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, ti
             "unique_experts": round(float(np.mean(uniq)), 2), "tokens": n_tok,
             "note": "4 tokens, own top-10 each + shared; each unique expert read once; "
                     "graph over the %d-layer stack" % NL}
+
+
+def mixed_arena(torch, synth, q4mi_ty_rb, E, H, F, tg, td, seed):
+    """An expert arena of E packed experts [gate F x H | up F x H | down H x F]
+    with gate/up blocks of type tg and down blocks of type td, generated in
+    HBM (uniform bytes, fp16 |N(0,1)| * 0.02 block scales)."""
+    rbg, rbd = q4mi_ty_rb(tg, H), q4mi_ty_rb(td, F)
+    stride = 2 * F * rbg + H * rbd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    a = torch.randint(0, 256, (E, stride), dtype=torch.uint8, device="cuda", generator=g)
+    for ty, lo, hi in ((tg, 0, 2 * F * rbg), (td, 2 * F * rbg, stride)):
+        vals, nb, doff = synth.BLOCKS[ty]
+        part = a[:, lo:hi].reshape(E, (hi - lo) // nb, nb)
+        d = (torch.randn(E, (hi - lo) // nb, device="cuda", generator=g).abs() * 0.02
+             ).to(torch.float16)
+        part[:, :, doff:doff + 2] = d.view(torch.uint8).view(E, (hi - lo) // nb, 2)
+        a[:, lo:hi] = part.reshape(E, hi - lo)
+    return a.view(-1), stride, 0, F * rbg, 2 * F * rbg
+
+
+def bench_window_mixes(L, torch, np, q4mi, synth, capture, timed, args, NL=24, n_tok=4):
+    """The 4-token verify window at the reference model's shapes (hidden 2560,
+    expert intermediate 640, 512 experts, top-10 + the shared expert) for the
+    gate/up formats the reference quotes its window on (IQ2_S / IQ3_XXS /
+    IQ3_S gate/up, IQ4_NL down: 46 / 51 / 53 us per layer on an RX 7900 XTX,
+    AGENTS.md:410-414 of the reference), over a stack of NL distinct-expert
+    layers (graph replay).  Bytes per layer = every unique expert once + x, y."""
+    H, F, E = 2560, 640, N_EXP + 1
+    rb = lambda ty, n: n // synth.BLOCKS[ty][0] * synth.BLOCKS[ty][1]
+    rng = np.random.default_rng(777)
+    es = np.full((NL, n_tok, 64), -1, np.int32)
+    ew = np.zeros((NL, n_tok, 64), np.float32)
+    nh = np.zeros((NL, n_tok), np.int32)
+    uniq = []
+    for l in range(NL):
+        ids_l = set()
+        for t, (ids, w) in enumerate(routes(rng, n_tok)):
+            es[l, t, :len(ids)], ew[l, t, :len(ids)], nh[l, t] = ids, w, len(ids)
+            ids_l.update(int(i) for i in ids)
+        uniq.append(len(ids_l))
+    d_es, d_ew, d_nh = (torch.from_numpy(a).cuda() for a in (es, ew, nh))
+    xs = torch.randn(NL, n_tok, H, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    ys = torch.zeros(NL, n_tok, H, device="cuda")
+    out = {"shape": "hidden 2560, n_ff 640, 512 experts top-10 + shared, 4 tokens",
+           "layers": NL}
+    TD = synth.T_IQ4_NL
+    for name, tg in (("IQ2_S", synth.T_IQ2_S), ("IQ3_XXS", synth.T_IQ3_XXS),
+                     ("IQ3_S", synth.T_IQ3_S)):
+        if not L.q4_hip_moe_win_ok(tg, tg, TD, H, F, n_tok):
+            out[name] = "not covered"
+            continue
+        arenas = []
+        for l in range(NL):
+            arenas.append(mixed_arena(torch, synth, rb, E, H, F, tg, TD, 900 + l))
+        stride, og, ou, od = arenas[0][1:]
+
+        def stack():
+            for l in range(NL):
+                q4mi.check(L.q4_hip_moe_exec_win(arenas[l][0].data_ptr(), stride,
+                                                 d_es[l].data_ptr(), d_ew[l].data_ptr(),
+                                                 d_nh[l].data_ptr(), n_tok, tg, og, tg, ou, TD,
+                                                 od, xs[l].data_ptr(), None, ys[l].data_ptr(),
+                                                 F, H, H), "q4_hip_moe_exec_win")
+        g = capture(stack)
+        steps = max(args.steps // 4, 10)
+        ms = timed(g, steps, max(args.warmup // 4, 2))
+        t = ms * 1e-3 / (steps * NL)
+        nbytes = float(np.mean(uniq)) * stride + 2 * 4 * n_tok * H
+        out[name] = {"layer_us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                     "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2)}
+        del g, arenas
+        torch.cuda.empty_cache()
+    out["reference_rx7900xtx_us"] = {"IQ2_S": 46, "IQ3_XXS": 51, "IQ3_S": 53}
+    return out
 
 
 def bench_gemv_lines():

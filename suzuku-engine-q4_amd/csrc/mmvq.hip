@@ -130,6 +130,7 @@ static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const fl
         return launch_ok("mmvq_k");                                                      \
     }
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+    Q4MI_L(16, 5) Q4MI_L(4, 5)
 #undef Q4MI_L
     set_error("mmvq: K=%u not covered", K);
     return false;

@@ -87,15 +87,17 @@ struct XRegs {
 
 // xq: [nt][K] int8, xd: [nt][K/32] (global or LDS); tokens >= nt read as 0.
 // Lane gi's groups: gi + TPR*m, or with ADJ the adjacent GPT*gi + m.
+// (G: the row's group count when TPR * GPT covers more groups than the row
+// has; the lanes past it hold zeros)
 template <int NT, int GPT, int TPR, bool ADJ = false>
 __device__ inline void load_xregs(XRegs<NT, GPT> &x, const int8_t *xq, const float *xd,
-                                  uint32_t K, uint32_t nt, uint32_t gi) {
+                                  uint32_t K, uint32_t nt, uint32_t gi, uint32_t G = ~0u) {
 #pragma unroll
     for (int m = 0; m < GPT; m++) {
         const uint32_t g = ADJ ? GPT * gi + m : gi + TPR * m;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if ((uint32_t)t < nt) {
+            if ((uint32_t)t < nt && g < G) {
                 const int4 a = *(const int4 *)(xq + (size_t)t * K + 32u * g);
                 const int4 b = *(const int4 *)(xq + (size_t)t * K + 32u * g + 16u);
                 x.q[m][t][0] = a.x; x.q[m][t][1] = a.y; x.q[m][t][2] = a.z; x.q[m][t][3] = a.w;
@@ -246,7 +248,10 @@ __device__ inline void reduce_acc(float (&acc)[NT]) {
     for (int t = 0; t < NT; t++) acc[t] = q4mi_rsum<TPR>(acc[t]);
 }
 
-// Layout of lanes over a row of G = K/32 groups.
+// Layout of lanes over a row of G = K/32 groups: TPR lanes (a power of two,
+// the DPP row-sum tree) with GPT groups each, TPR * GPT = G.  Besides the
+// power-of-two rows, the reference model's hidden 2560 (80 groups: 16 x 5)
+// and expert intermediate 640 (20 groups: 4 x 5).
 struct RowLayout {
     int tpr, gpt;
 };
@@ -254,6 +259,8 @@ inline RowLayout layout_for(uint32_t G) {
     if (G == 8 || G == 16 || G == 32 || G == 64) return {(int)G, 1};
     if (G == 128) return {64, 2};
     if (G == 256) return {64, 4};
+    if (G == 80) return {16, 5};
+    if (G == 20) return {4, 5};
     return {0, 0};
 }
 

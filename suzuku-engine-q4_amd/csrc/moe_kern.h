@@ -62,7 +62,8 @@ constexpr uint32_t kT = Q4MI_THREADS;   // threads per block
 constexpr uint32_t kProd = Q4MI_PROD;   // producer waves (issue the LDS copies)
 constexpr uint32_t kCons = kT - kProd * 64;   // consumer threads
 constexpr uint32_t kConsW = kCons / 64;       // consumer waves
-constexpr uint32_t kDnRows = 8;   // output rows per down block
+constexpr uint32_t kDnRows = 8;       // output rows per down block (a call may take more)
+constexpr uint32_t kDnRowsMax = 16;   // ... up to this many, so the grid fits the CUs
 constexpr uint32_t kMaxS = 32;    // LDS ring slots
 struct HostList {
     int32_t id[kMaxU];
@@ -396,6 +397,7 @@ struct MoeArgs {
     uint32_t ahead;   // chunks a producer may have issued and not yet published (<= kMaxS)
     uint32_t slots;   // LDS ring slots (<= kMaxS)
     uint32_t nsel_cap;  // down: q8(h) rows the LDS holds
+    uint32_t dn_rows;   // down: output rows per block (kDnRows .. kDnRowsMax)
     const float *x;   // [n_tok][K]
     float *h;         // [kMaxU][kMaxT][n_ff] fp32 h
     float *y;         // [n_tok][n_embd], accumulated
@@ -704,7 +706,10 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     // groups GPT*gi + m, decoded in pairs that share their superblock reads
     constexpr bool kPair = TY == Q4MI_T_IQ3_S && GPT % 2 == 0;
     XRegs<NT, GPT> xr;
-    load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi);
+    // a layout may cover more groups than the row has (TPR * GPT > G):
+    // lanes past the row skip their groups
+    const uint32_t G = K / 32;
+    load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi, G);
     float *hout = a.h;
 #ifdef Q4MI_TRACE
     unsigned long long *const q4tr = a.trace;
@@ -749,6 +754,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
 #pragma unroll
                 for (int m = 0; m < GPT; m += 2) {
                     const uint32_t g = GPT * gi + m;
+                    if (g >= G) continue;   // (G is even: both groups or neither)
 #pragma unroll
                     for (int which = 0; which < 2; which++) {
                         int32_t wa[8], wb[8];
@@ -763,6 +769,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
 #pragma unroll
                 for (int m = 0; m < GPT; m++) {
                     const uint32_t g = gi + TPR * m;
+                    if (g >= G) continue;
 #pragma unroll
                     for (int which = 0; which < 2; which++) {
                         int32_t w[8];
@@ -855,21 +862,21 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
 
 // ---------------------------------------------------------------- down
 // Same roles.  Items are (expert u, output row rr); the chunks are runs of
-// `ch` experts (kDnRows rows each).  The consumers quantize every selected
+// `ch` experts (dn_rows rows each).  The consumers quantize every selected
 // h row (q8, 32-value groups) into LDS before computing.
 //
-// LDS: [stab] Plan Sync | part [kMaxU][NT][kDnRows] | hq [nsel_cap][n_ff] |
-//      hd [nsel_cap][n_ff/32] | ring of S slots, slot = ch experts x kDnRows
+// LDS: [stab] Plan Sync | part [kMaxU][NT][dn_rows] | hq [nsel_cap][n_ff] |
+//      hd [nsel_cap][n_ff/32] | ring of S slots, slot = ch experts x dn_rows
 //      rows.
 //
-// Block `bid` owns output rows 8*bid..8*bid+7.
+// Block `bid` owns output rows dn_rows*bid .. dn_rows*bid + dn_rows - 1.
 template <uint32_t UNIT>
 __device__ inline void dn_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *ring, uint32_t ch,
                                   uint32_t S, int32_t idv, uint32_t nu, uint32_t r0, uint32_t nr,
                                   uint32_t wave, uint32_t lane) {
     const uint8_t *base = a.base;
     const uint64_t stride = a.stride_d, od = a.od;
-    const uint32_t rb = a.rb_dn, slot_bytes = ch * kDnRows * rb;
+    const uint32_t rb = a.rb_dn, slot_bytes = ch * a.dn_rows * rb;
     const uint32_t C = (nu + ch - 1) / ch;
     uint32_t issued = 0;
     auto issue = [&](uint32_t c) {
@@ -907,7 +914,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
                                   uint32_t nsel, bool uniq, float wv, float yv, float4 v0,
                                   float4 v1, bool pre, uint32_t ct, uint32_t cw, uint32_t lane) {
     const uint32_t n_ff = a.n_ff, rb = a.rb_dn, nt = a.src.n_tok;
-    const uint32_t slot_bytes = ch * kDnRows * rb;
+    const uint32_t dr = a.dn_rows, slot_bytes = ch * dr * rb;
     const float *hg = a.h;
     const uint32_t qpr = n_ff / 4;
     // host list: its weights go to Plan::w[0] for the final sum
@@ -1005,7 +1012,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const float v = ((sel >> t) & 1u) ? q4mi_rsum<TPR>(acc[t]) : 0.f;
-                if (gi == TPR - 1) part[((size_t)u * NT + t) * kDnRows + rr] = v;
+                if (gi == TPR - 1) part[((size_t)u * NT + t) * dr + rr] = v;
             }
             if (gi == TPR - 1) atomicAdd(&Y->cons[c % S], 1u);
         }
@@ -1025,7 +1032,7 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
         const uint32_t o = c8 >> 3, sl = c8 & 7u, t = o / nr, rr = o % nr;
         float s = 0.f;
         for (uint32_t u = sl; u < nu; u += 8)
-            if (uniq || ((P->sel[u] >> t) & 1u)) s += P->w[t][u] * part[((size_t)u * NT + t) * kDnRows + rr];
+            if (uniq || ((P->sel[u] >> t) & 1u)) s += P->w[t][u] * part[((size_t)u * NT + t) * dr + rr];
         s = q4mi_rsum<8>(s);
         // outputs past the first kCons / 8 read their old y here
         const float y0 = c8 == ct ? yv : a.y[(size_t)t * a.n_embd + r0 + rr];
@@ -1053,15 +1060,15 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     uint32_t *stab = (uint32_t *)smem;
     Plan *P = (Plan *)(smem + tab_bytes<TY>());
     Sync *Y = (Sync *)(P + 1);
-    float *part = (float *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));   // [kMaxU][NT][kDnRows]
-    int8_t *hq = (int8_t *)(part + kMaxU * NT * kDnRows);
+    float *part = (float *)(smem + al16((size_t)((uint8_t *)(Y + 1) - smem)));   // [kMaxU][NT][dn_rows]
+    int8_t *hq = (int8_t *)(part + kMaxU * NT * a.dn_rows);
     const uint32_t n_ff = a.n_ff, cap = a.nsel_cap;
     float *hd = (float *)(hq + (size_t)cap * n_ff);
     uint8_t *ring = smem + al16((size_t)((uint8_t *)(hd + (size_t)cap * (n_ff / 32)) - smem));
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t r0 = bid * kDnRows;
-    const uint32_t nr = min(kDnRows, a.n_embd - r0);
+    const uint32_t r0 = bid * a.dn_rows;
+    const uint32_t nr = min(a.dn_rows, a.n_embd - r0);
     const KArgs ka = kargs();
     const bool uniq = a.src.unique != 0;
     // the host list's ids (producers) or weights (consumers), loaded while
@@ -1170,7 +1177,7 @@ template <int NT>
 static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &ch, uint32_t &S,
                       uint32_t ty) {
     const uint32_t cap = nu_host ? nu_host : kMaxU;   // selected pairs (<= 64)
-    const size_t fixed = head_bytes(ty) + (size_t)kMaxU * NT * kDnRows * 4 +
+    const size_t fixed = head_bytes(ty) + (size_t)kMaxU * NT * a.dn_rows * 4 +
                          al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
     const uint32_t nu_est = nu_host ? nu_host : kMaxU;
     ch = std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd);
@@ -1179,16 +1186,16 @@ static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &
 #endif
     S = 0;
     for (;; ch = (ch + 1) / 2) {
-        const size_t slot = (size_t)ch * kDnRows * a.rb_dn;
+        const size_t slot = (size_t)ch * a.dn_rows * a.rb_dn;
         S = fixed < cap_bytes ? (uint32_t)std::min<size_t>(kMaxS, (cap_bytes - fixed) / slot) : 0;
         if (S >= 2 || ch == 1) break;
     }
-    // a consumer wave's 64/TPR (<= 8) consecutive items touch at most two chunks (ch * kDnRows >= 8)
+    // a consumer wave's 64/TPR consecutive items may touch several chunks (it waits for each)
     const uint32_t C = (nu_est + ch - 1) / ch;
     if (S < 2 && S < C) return 0;
     S = std::min<uint32_t>(S, std::max<uint32_t>(1, C));
     a.nsel_cap = cap;
-    return std::max(fixed + (size_t)S * ch * kDnRows * a.rb_dn, fixed + kPlanTable);
+    return std::max(fixed + (size_t)S * ch * a.dn_rows * a.rb_dn, fixed + kPlanTable);
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>
@@ -1218,6 +1225,12 @@ static bool launch_gu(MoeArgs a, uint32_t nu_host) {
 
 template <uint32_t TY, int NT, int TPR, int GPT>
 static bool launch_dn(MoeArgs a, uint32_t nu_host) {
+    // rows per block: 8, or more (up to 16) when 8 would need more blocks
+    // than CUs (hidden 2560: 10 rows, 256 blocks; 4096: 16)
+    const uint32_t cus = (uint32_t)cu_count();
+    a.dn_rows = kDnRows;
+    if ((a.n_embd + kDnRows - 1) / kDnRows > cus)
+        a.dn_rows = std::min(kDnRowsMax, (a.n_embd + cus - 1) / cus);
     uint32_t ch, S;
     const size_t lds = dn_plan<NT>(a, nu_host, lds_cap(), ch, S, TY);
     if (!lds) {
@@ -1226,17 +1239,17 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
     }
     a.chunk = ch;
     a.slots = S;
-    // a block copies one contiguous run of kDnRows rows per expert: 16-byte
+    // a block copies one contiguous run of dn_rows rows per expert: 16-byte
     // units need that run (not each row) 16-byte aligned and sized
-    const bool wide = ((((uintptr_t)a.base) | a.stride_d | a.od | ((uint64_t)kDnRows * a.rb_dn)) & 15u) == 0 &&
-                      a.n_embd % kDnRows == 0;
+    const bool wide = ((((uintptr_t)a.base) | a.stride_d | a.od | ((uint64_t)a.dn_rows * a.rb_dn)) & 15u) == 0 &&
+                      a.n_embd % a.dn_rows == 0;
     const void *fn = wide ? (const void *)moe_dn_k<TY, NT, TPR, GPT, 16>
                           : (const void *)moe_dn_k<TY, NT, TPR, GPT, 4>;
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         set_error("moe_dn_k: LDS limit (%zu)", lds);
         return false;
     }
-    const uint32_t grid = (a.n_embd + kDnRows - 1) / kDnRows;
+    const uint32_t grid = (a.n_embd + a.dn_rows - 1) / a.dn_rows;
     if (wide)
         moe_dn_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
     else
@@ -1251,6 +1264,10 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
 static RowLayout gu_layout(uint32_t G, int NT) {
     const uint32_t gn = (G / 32) * (uint32_t)NT;
     if (G >= 64 && G % 32 == 0 && (gn <= 4 || (NT == 4 && G == 64))) return RowLayout{32, (int)(G / 32)};
+    // 80 groups (hidden 2560) for several tokens: 64 lanes x 2 groups with the
+    // last 48 slots idle, so x stays in registers (16 x 5 would hold 5 groups
+    // per token and spill)
+    if (G == 80 && NT >= 2) return RowLayout{64, 2};
     return layout_for(G);
 }
 
@@ -1260,6 +1277,7 @@ static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_gu<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+    Q4MI_L(16, 5)
     if constexpr (NT <= 4) { Q4MI_L(32, 2) }
     if constexpr (NT == 1) { Q4MI_L(32, 4) }
 #undef Q4MI_L
@@ -1283,6 +1301,7 @@ static bool dn_dispatch(const MoeArgs &a, uint32_t nu_host) {
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_dn<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
+    Q4MI_L(4, 5)
     if constexpr (NT <= 4) { Q4MI_L(8, 2) }
 #undef Q4MI_L
     return false;

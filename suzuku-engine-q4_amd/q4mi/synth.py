@@ -104,6 +104,20 @@ def device_iq3s(nbytes, seed, device="cuda"):
     return b.view(-1)
 
 
+def device_blocks(ty, nblocks, seed, device="cuda"):
+    """Blocks of any format in BLOCKS generated in HBM: uniform bytes with an
+    fp16 |N(0,1)| * 0.02 block scale (every index, sign, sub-block scale and
+    quant field then uniform over its range)."""
+    import torch
+    vals, nb, doff = BLOCKS[ty]
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    b = torch.randint(0, 256, (nblocks, nb), dtype=torch.uint8, device=device, generator=g)
+    d = (torch.randn(nblocks, device=device, generator=g).abs() * 0.02).to(torch.float16)
+    b[:, doff:doff + 2] = d.view(torch.uint8).view(nblocks, 2)
+    return b.view(-1)
+
+
 def device_q80(nbytes, seed, device="cuda"):
     import torch
     g = torch.Generator(device=device)
