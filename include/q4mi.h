@@ -54,7 +54,8 @@ bool q4mi_quant8(const float *d_x, const int32_t *d_ids, uint64_t rows, uint64_t
 /* Replaces q4_mmvq_on/_set/_verify/_warm/_hold/_release/q4_mmvq_n
  * (src/q4.h:914-927, src/q4_mmvq.cu:266-349), extended to IQ3_S and Q8_0:
  * y[t*nrows + r] = scale * (W_r . q8(x_t)), t < n (1..8).  A row's result
- * does not depend on n.  ncols/32 in {8,16,32,64,128,256}. */
+ * does not depend on n.  ncols/32 in {8,16,32,64,128,256} or 20 / 80 (the
+ * reference model's 640 and 2560). */
 int q4_mmvq_on(void);
 void q4_mmvq_set(int v);
 void q4_mmvq_verify(int on);
