@@ -131,6 +131,8 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
         (void)hipMemset(g_trace, 0, 2 * 4096 * 32 * 8);
     a.trace = g_trace;
     a.dbg = getenv("Q4MI_DBG") ? (uint32_t)atoi(getenv("Q4MI_DBG")) : 0u;
+#endif
+#if defined(Q4MI_TRACE) || defined(Q4MI_KNOBS)
     if (getenv("Q4MI_AHEAD")) a.ahead = (uint32_t)atoi(getenv("Q4MI_AHEAD"));
 #endif
     const uint32_t nt = src.n_tok;
