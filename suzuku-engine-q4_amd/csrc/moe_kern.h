@@ -65,6 +65,10 @@ constexpr uint32_t kConsW = kCons / 64;       // consumer waves
 constexpr uint32_t kDnRows = 8;       // output rows per down block (a call may take more)
 constexpr uint32_t kDnRowsMax = 16;   // ... up to this many, so the grid fits the CUs
 constexpr uint32_t kMaxS = 32;    // LDS ring slots
+// x quads per consumer thread loaded before the block barrier: all of a
+// window's, and a decode token's with the least prologue code (the prologue
+// runs with a cold instruction cache, on the critical path)
+template <int NT> constexpr uint32_t kXPre = NT == 1 ? 1u : 4u;
 struct HostList {
     int32_t id[kMaxU];
     float w[kMaxU];
@@ -98,6 +102,18 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *h
     // every token's count in one load (lane t holds token t's), then
     // read back lane by lane: one memory round trip, not one per token
     const int cnt_l = lane < s.n_tok ? (s.nh ? s.nh[lane] : (int)s.n_fixed) : 0;
+    // the entries are loaded in the same round trip as the counts, assuming
+    // each token has at most CAP = 64 / (n_tok rounded up to a power of two)
+    // of them (lane l: token l / CAP, entry l % CAP; within the lists' rows);
+    // a longer list loads them again once the counts are known
+    const uint32_t cap_sh = s.n_tok <= 1 ? 6u : s.n_tok == 2 ? 5u : s.n_tok <= 4 ? 4u : 3u;
+    const uint32_t st = lane >> cap_sh, sr = lane & ((1u << cap_sh) - 1u);
+    int32_t sid = -1;
+    float sw = 0.f;
+    if (st < s.n_tok && sr < s.stride) {
+        sid = s.es[(size_t)st * s.stride + sr];
+        sw = s.ew[(size_t)st * s.stride + sr];
+    }
     uint32_t E = 0, tok = 0, rem = 0;
     bool found = false;
     for (uint32_t t = 0; t < s.n_tok; t++) {
@@ -114,7 +130,15 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *h
     if (E > kMaxU) E = kMaxU;
     int32_t id = -1;
     float w = 0.f;
-    if (lane < E) {
+    if (__ballot(lane < E && rem >= (1u << cap_sh)) == 0) {
+        const int src = (int)((tok << cap_sh) + rem);
+        const int32_t gid = __shfl(sid, src);
+        const float gw = __shfl(sw, src);
+        if (lane < E) {
+            id = gid;
+            w = gw;
+        }
+    } else if (lane < E) {
         id = s.es[(size_t)tok * s.stride + rem];
         w = s.ew[(size_t)tok * s.stride + rem];
     }
@@ -668,16 +692,18 @@ __device__ inline void gu_produce(const MoeArgs &a, Plan *P, Sync *Y, uint8_t *r
     );
 }
 
-// Consumer prologue: q8 of x (v0 = quad ct, loaded by the caller), then
-// wait until every consumer wave finished the shared tables.
+// Consumer prologue: q8 of x (v[k] = quad ct + k kCons, loaded by the
+// caller), then wait until every consumer wave finished the shared tables.
 template <int NT>
-__device__ inline void gu_quant_x(const MoeArgs &a, Sync *Y, int8_t *xq, float *xd, float4 v0,
-                                  uint32_t ct, uint32_t lane) {
+__device__ inline void gu_quant_x(const MoeArgs &a, Sync *Y, int8_t *xq, float *xd,
+                                  const float4 (&v0)[kXPre<NT>], uint32_t ct, uint32_t lane) {
     const uint32_t nq = a.src.n_tok * a.K / 4;
     const float4 *xg = (const float4 *)a.x;
-    if (ct < nq) quant_quad(v0, ct, xq, xd);
-    // further quads (several tokens) four loads in flight at a time
-    for (uint32_t i0 = ct + kCons; i0 < nq; i0 += 4 * kCons) {
+#pragma unroll
+    for (uint32_t k = 0; k < kXPre<NT>; k++)
+        if (ct + k * kCons < nq) quant_quad(v0[k], ct + k * kCons, xq, xd);
+    // further quads (many tokens) four loads in flight at a time
+    for (uint32_t i0 = ct + kXPre<NT> * kCons; i0 < nq; i0 += 4 * kCons) {
         float4 v[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -815,15 +841,24 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     // after the barrier
     const uint32_t nq = a.src.n_tok * a.K / 4;
     uint32_t code = 0u;
-    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v0[kXPre<NT>];
+#pragma unroll
+    for (uint32_t k = 0; k < kXPre<NT>; k++) v0[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (wave >= kProd) {
         const uint32_t c0 = tid - kProd * 64;
         if (kIq && c0 < 512) code = q4mi_iq3s_code_dev[c0];
-        if (c0 < nq) v0 = ((const float4 *)a.x)[c0];
+        // every x quad of up to kXPre<NT> passes: loads issued after the
+        // barrier queue behind the weight stream and return when it drains
+#pragma unroll
+        for (uint32_t k = 0; k < kXPre<NT>; k++)
+            if (c0 + k * kCons < nq) v0[k] = ((const float4 *)a.x)[c0 + k * kCons];
     }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
     if (!uniq && tid < 64) build_plan(P, a.src, tid, (uint32_t *)ring);
+    Q4MI_TR(13, 0, tid == 0);
+    Q4MI_TR(14, 0, tid == kProd * 64);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
+    Q4MI_TR(15, 0, tid == 0);
     if (!uniq && bid == 0 && wave == kProd) {   // the down launch reuses this plan
         for (uint32_t i = lane; i < sizeof(Plan) / 16; i += 64)
             ((uint4 *)a.gplan)[i] = ((const uint4 *)P)[i];
@@ -928,14 +963,17 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
         const uint32_t row = uniq ? s * kMaxT : P->prow[s];
         return ((const float4 *)(hg + (size_t)row * n_ff))[i % qpr];
     };
-    if (!pre) {
-        if (ct < nq) v0 = hquad(ct);
-        if (ct + kCons < nq) v1 = hquad(ct + kCons);
+    // device lists: the rows are known only now, and these loads queue
+    // behind the weight stream, so the first batch takes eight quads per
+    // thread (a window's 44 rows in one round trip)
+    uint32_t i0 = ct;
+    if (pre) {
+        if (ct < nq) quant_quad(v0, ct, hq, hd);
+        if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
+        i0 = ct + 2 * kCons;
     }
-    if (ct < nq) quant_quad(v0, ct, hq, hd);
-    if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
-    // further quads (many pairs) eight loads in flight at a time
-    for (uint32_t i0 = ct + 2 * kCons; i0 < nq; i0 += 8 * kCons) {
+    // further quads eight loads in flight at a time
+    for (; i0 < nq; i0 += 8 * kCons) {
         float4 v[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
