@@ -9,6 +9,15 @@
 
 namespace q4mi {
 
+// Optional build (-DQ4MI_GTRACE): thread 0 of each of the first 1024 blocks
+// records wall-clock phase timestamps (10 ns ticks) of the last call.
+#ifdef Q4MI_GTRACE
+static __device__ unsigned long long g_gtr[1024 * 8];
+#define Q4MI_GTR(k) do { if (threadIdx.x == 0 && blockIdx.x < 1024) g_gtr[blockIdx.x * 8 + (k)] = wall_clock64(); } while (0)
+#else
+#define Q4MI_GTR(k) do { } while (0)
+#endif
+
 bool quant8_launch(const float *x, const int32_t *ids, uint64_t rows, uint32_t cols,
                    int8_t *q, float *d, int32_t *bs);
 
@@ -17,8 +26,8 @@ bool quant8_launch(const float *x, const int32_t *ids, uint64_t rows, uint32_t c
 // bit), so a call needs no separate quantize launch; else xq / xd hold them.
 // (Two instantiations: the in-block quantizer's batched loads take 32
 // registers, which the pre-quantized kernel does not pay for.)
-template <class F, int NT, int TPR, int GPT, bool XF>
-__global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uint32_t rows,
+template <class F, int NT, int TPR, int GPT, bool XF, int NTHR>
+__global__ __launch_bounds__(NTHR) void mmvq_k(const uint8_t *__restrict__ W, uint32_t rows,
                                               uint32_t K, uint32_t rb, uint32_t R,
                                               const float *__restrict__ xf,
                                               const int8_t *__restrict__ xq,
@@ -37,9 +46,12 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
     // return when the copies have landed (measured: copies first, or copies
     // from fewer waves while the others build the table and quantize, are
     // slower for configs[0]).
-    F::init(tab, tid, 256);
-    stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, 256);
-    const uint32_t hid = tid, nh = 256u;
+    Q4MI_GTR(0);
+    F::init(tab, tid, NTHR);
+    Q4MI_GTR(1);
+    stage_tile_issue(tile, W + (size_t)r0 * rb, nr * rb, tid, NTHR);
+    Q4MI_GTR(2);
+    const uint32_t hid = tid, nh = NTHR;
     const uint32_t gi = tid % TPR;
     XRegs<NT, GPT> x;
     // pre-quantized codes: loaded while the tile copy is in flight
@@ -80,10 +92,13 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
         xq = (const int8_t *)(tile + ((R * rb + 15u) & ~15u));
         xd = (const float *)(xq + (size_t)NT * K);
     }
+    Q4MI_GTR(3);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    Q4MI_GTR(4);
     __syncthreads();
+    Q4MI_GTR(5);
     if constexpr (XF) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
-    for (uint32_t rr = tid / TPR; rr < nr; rr += 256 / TPR) {
+    for (uint32_t rr = tid / TPR; rr < nr; rr += NTHR / TPR) {
         float acc[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[t] = 0.f;
@@ -97,6 +112,7 @@ __global__ __launch_bounds__(256) void mmvq_k(const uint8_t *__restrict__ W, uin
                 if ((uint32_t)t < nt) y[(size_t)t * rows + r0 + rr] = scale * acc[t];
         }
     }
+    Q4MI_GTR(6);
 }
 
 // weight bytes per row tile
@@ -111,22 +127,57 @@ static bool mmvq_launch_nt(const uint8_t *W, uint32_t rows, uint32_t K, const fl
     const uint32_t G = K / 32;
     const RowLayout L = layout_for(G);
     const uint32_t rb = (uint32_t)q4mi_row_bytes(F::kType, K);
-    const uint32_t target = tile_target(F::kType);
-    const uint32_t R = tile_rows(rb, L.tpr, target);
     const size_t xlds = xf ? (size_t)NT * K + (size_t)NT * (K / 32) * 4 : 0;
-    const size_t lds = F::kTabBytes + (((size_t)R * rb + 15) & ~(size_t)15) +
-                       xlds + 64;
-    const dim3 grid((rows + R - 1) / R), blk(256);
+    auto lds_of = [&](uint32_t r) {
+        return F::kTabBytes + (((size_t)r * rb + 15) & ~(size_t)15) + xlds + 64;
+    };
+    uint32_t nthr = 256;
+    uint32_t R = L.tpr ? tile_rows(rb, L.tpr, tile_target(F::kType)) : 1;
+    // fp32 x (the short matrices): a 1024-thread block per 1024 / tpr rows
+    // (one row per wave) while that still fills the CUs, else 512 threads
+    // per 512 / tpr rows.  The compute after a tile lands is then a quarter
+    // (a half) of a 256-thread block's, whose waves take four rows each
+    // (configs[0]: 256 blocks of 16 rows, 6.2 against 7.1 us).  Several
+    // tokens' x registers fit 1024-thread blocks (128 VGPRs) only at one
+    // token, 512-thread blocks up to two.
+    if (xf && L.tpr) {
+        const uint32_t cus = (uint32_t)cu_count();
+        for (uint32_t n = 1024; n >= 512; n /= 2) {
+            const uint32_t r = n / (uint32_t)L.tpr;
+            if ((n == 1024 ? NT == 1 : NT <= 2) && (rows + r - 1) / r >= cus && lds_of(r) <= 65536) {
+                nthr = n;
+                R = r;
+                break;
+            }
+        }
+    }
+#ifdef Q4MI_KNOBS
+    if (getenv("Q4MI_GEMV_NTHR") && xf && L.tpr && NT == 1) {
+        nthr = (uint32_t)atoi(getenv("Q4MI_GEMV_NTHR"));
+        R = tile_rows(rb, L.tpr, getenv("Q4MI_GEMV_TILE") ? (uint32_t)atoi(getenv("Q4MI_GEMV_TILE"))
+                                                          : tile_target(F::kType), nthr);
+    }
+#endif
+    const size_t lds = lds_of(R);
+    const dim3 grid((rows + R - 1) / R), blk(nthr);
 #define Q4MI_L(T, P)                                                                     \
     if (L.tpr == T && L.gpt == P) {                                                      \
-        if (xf)                                                                          \
-            mmvq_k<F, NT, T, P, true><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, \
-                                                                    xq, xd, nt, y, scale, \
-                                                                    sums);               \
-        else                                                                             \
-            mmvq_k<F, NT, T, P, false><<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, \
-                                                                     xq, xd, nt, y, scale, \
-                                                                     sums);              \
+        const auto args = [&](auto kern) {                                               \
+            kern<<<grid, blk, lds, stream()>>>(W, rows, K, rb, R, xf, xq, xd, nt, y, scale, sums); \
+        };                                                                               \
+        if constexpr (NT == 1) {                                                         \
+            if (xf && nthr == 1024) args(mmvq_k<F, NT, T, P, true, 1024>);              \
+            else if (xf && nthr == 512) args(mmvq_k<F, NT, T, P, true, 512>);           \
+            else if (xf) args(mmvq_k<F, NT, T, P, true, 256>);                          \
+            else args(mmvq_k<F, NT, T, P, false, 256>);                                 \
+        } else if constexpr (NT == 2) {                                                  \
+            if (xf && nthr == 512) args(mmvq_k<F, NT, T, P, true, 512>);                \
+            else if (xf) args(mmvq_k<F, NT, T, P, true, 256>);                          \
+            else args(mmvq_k<F, NT, T, P, false, 256>);                                 \
+        } else {                                                                         \
+            if (xf) args(mmvq_k<F, NT, T, P, true, 256>);                               \
+            else args(mmvq_k<F, NT, T, P, false, 256>);                                 \
+        }                                                                                \
         return launch_ok("mmvq_k");                                                      \
     }
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
@@ -281,3 +332,12 @@ bool q4mi_mmvq(uint32_t ty, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
 }
 
 }  // extern "C"
+
+#ifdef Q4MI_GTRACE
+/* GEMV trace build only: the phase timestamps [1024 blocks][8] of the last
+ * call. */
+extern "C" bool q4mi_gtrace_read(unsigned long long *dst) {
+    if (hipDeviceSynchronize() != hipSuccess) return false;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(q4mi::g_gtr), sizeof(q4mi::g_gtr)) == hipSuccess;
+}
+#endif

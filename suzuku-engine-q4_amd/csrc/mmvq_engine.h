@@ -266,8 +266,8 @@ inline RowLayout layout_for(uint32_t G) {
 
 // Rows per block so that a tile is about `target` bytes, a multiple of the
 // rows one pass covers (256 / tpr).
-inline uint32_t tile_rows(uint32_t rb, int tpr, uint32_t target) {
-    const uint32_t rpp = 256u / (uint32_t)tpr;
+inline uint32_t tile_rows(uint32_t rb, int tpr, uint32_t target, uint32_t nthr = 256) {
+    const uint32_t rpp = nthr / (uint32_t)tpr;
     uint32_t r = target / rb;
     r = r / rpp * rpp;
     if (r < rpp) r = rpp;
