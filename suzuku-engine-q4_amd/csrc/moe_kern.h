@@ -731,11 +731,15 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     // IQ3_S with an even group count per lane: lane gi takes the adjacent
     // groups GPT*gi + m, decoded in pairs that share their superblock reads
     constexpr bool kPair = TY == Q4MI_T_IQ3_S && GPT % 2 == 0;
+    // five groups per lane at several tokens (80-group rows, 16 x 5): x is
+    // read from LDS per group, for the selected tokens only, since five
+    // groups of every token's x do not fit the registers
+    constexpr bool kXL = NT >= 2 && GPT == 5;
     XRegs<NT, GPT> xr;
     // a layout may cover more groups than the row has (TPR * GPT > G):
     // lanes past the row skip their groups
     const uint32_t G = K / 32;
-    load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi, G);
+    if constexpr (!kXL) load_xregs<NT, GPT, TPR, kPair>(xr, xq, xd, K, nt, gi, G);
     float *hout = a.h;
 #ifdef Q4MI_TRACE
     unsigned long long *const q4tr = a.trace;
@@ -765,16 +769,20 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
             float ag[NT], au[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.f;
-            auto dot = [&](int m, int which, const int32_t (&w)[8], int mult, int mult2,
-                           float d) __attribute__((always_inline)) {
+            auto dotx = [&](const auto &X, int m, int which, const int32_t (&w)[8], int mult,
+                            int mult2, float d) __attribute__((always_inline)) {
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     if (!((sel >> t) & 1u)) continue;
-                    const int s = tsum<TY>(w, xr.q[m][t], mult, mult2);
-                    const float f = (float)s * (d * xr.d[m][t]);
+                    const int s = tsum<TY>(w, X.q[m][t], mult, mult2);
+                    const float f = (float)s * (d * X.d[m][t]);
                     if (which == 0) ag[t] += f;
                     else au[t] += f;
                 }
+            };
+            auto dot = [&](int m, int which, const int32_t (&w)[8], int mult, int mult2,
+                           float d) __attribute__((always_inline)) {
+                dotx(xr, m, which, w, mult, mult2, d);
             };
             if constexpr (kPair) {
 #pragma unroll
@@ -796,13 +804,27 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
                 for (int m = 0; m < GPT; m++) {
                     const uint32_t g = gi + TPR * m;
                     if (g >= G) continue;
+                    XRegs<NT, 1> xl;
+                    if constexpr (kXL) {
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            if (!((sel >> t) & 1u)) continue;
+                            const int4 qa = *(const int4 *)(xq + (size_t)t * K + 32u * g);
+                            const int4 qb = *(const int4 *)(xq + (size_t)t * K + 32u * g + 16u);
+                            xl.q[0][t][0] = qa.x; xl.q[0][t][1] = qa.y; xl.q[0][t][2] = qa.z;
+                            xl.q[0][t][3] = qa.w; xl.q[0][t][4] = qb.x; xl.q[0][t][5] = qb.y;
+                            xl.q[0][t][6] = qb.z; xl.q[0][t][7] = qb.w;
+                            xl.d[0][t] = xd[(size_t)t * G + g];
+                        }
+                    }
 #pragma unroll
                     for (int which = 0; which < 2; which++) {
                         int32_t w[8];
                         int mult, mult2;
                         float d;
                         group_w<TY>(stab, tile, tw, __umul24(which * ch + j, rb), g, w, mult, mult2, d);
-                        dot(m, which, w, mult, mult2, d);
+                        if constexpr (kXL) dotx(xl, 0, which, w, mult, mult2, d);
+                        else dot(m, which, w, mult, mult2, d);
                     }
                 }
             }
@@ -1305,19 +1327,23 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
 // wave, so each wave has two pairs' chains in flight) while the activation
 // registers stay small (groups x tokens <= 4, or 2 groups x 4 tokens), else
 // the row layout.
-static RowLayout gu_layout(uint32_t G, int NT) {
+static RowLayout gu_layout(uint32_t G, int NT, uint32_t ty) {
     const uint32_t gn = (G / 32) * (uint32_t)NT;
     if (G >= 64 && G % 32 == 0 && (gn <= 4 || (NT == 4 && G == 64))) return RowLayout{32, (int)(G / 32)};
-    // 80 groups (hidden 2560) for several tokens: 64 lanes x 2 groups with the
-    // last 48 slots idle, so x stays in registers (16 x 5 would hold 5 groups
-    // per token and spill)
-    if (G == 80 && NT >= 2) return RowLayout{64, 2};
+    // 80 groups (hidden 2560) for several tokens.  IQ3_S: 64 lanes x 2
+    // adjacent groups (its paired decode) with the last 48 slots idle, x in
+    // registers; the other types: 16 lanes x 5 groups, every slot busy, x
+    // read from LDS per group (five groups of every token's x would spill).
+    // 4-token window at the reference model's shapes, gate/up alone: IQ3_S
+    // 28.9 / 30.1 us, IQ3_XXS 31.6 / 27.8 us, IQ2_S 31.0 / 25.9 us (64 x 2 /
+    // 16 x 5).
+    if (G == 80 && NT >= 2) return ty == Q4MI_T_IQ3_S ? RowLayout{64, 2} : RowLayout{16, 5};
     return layout_for(G);
 }
 
 template <uint32_t TY, int NT>
 static bool gu_dispatch(const MoeArgs &a, uint32_t nu_host) {
-    const RowLayout L = gu_layout(a.K / 32, NT);
+    const RowLayout L = gu_layout(a.K / 32, NT, TY);
 #define Q4MI_L(T, P) \
     if (L.tpr == T && L.gpt == P) return launch_gu<TY, NT, T, P>(a, nu_host);
     Q4MI_L(8, 1) Q4MI_L(16, 1) Q4MI_L(32, 1) Q4MI_L(64, 1) Q4MI_L(64, 2) Q4MI_L(64, 4)
