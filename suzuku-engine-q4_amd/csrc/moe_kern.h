@@ -1206,15 +1206,19 @@ static size_t head_bytes(uint32_t ty) {
 // `cap` bytes of LDS; returns the LDS bytes (0: does not fit).
 template <int NT>
 static size_t gu_plan(const MoeArgs &a, uint32_t nu_host, uint32_t grid, size_t cap,
-                      uint32_t &ch, uint32_t &S, uint32_t ty) {
+                      uint32_t &ch, uint32_t &S, uint32_t ty, uint32_t tpw) {
     // one chunk per producer wave when it fits (a producer publishes a chunk
     // only after issuing everything before it, so a second chunk would
-    // delay the first); device lists (unknown share) use 4 pairs, so the
-    // window's larger shares land chunk by chunk while the consumers work
-    // (measured, 4-token window: 4 / 8 / 16 pairs 34.5 / 34.8 / 35.6 us)
+    // delay the first); device lists (unknown share) use small chunks, so
+    // the window's larger shares land chunk by chunk while the consumers
+    // work: 4 pairs, or two waves' worth when a wave takes more than two
+    // pairs a round (tpw).  Measured, 4-token windows: configs[2] (2 pairs
+    // per wave) 4 / 8 / 16 pairs 34.5 / 34.8 / 35.6 us; at hidden 2560,
+    // IQ3_S (1 pair per wave) 4 / 8 pairs 29.0 / 29.8 us gate/up, IQ3_XXS and
+    // IQ2_S (4 pairs per wave) 27.9 / 26.2 and 26.1 / 24.5 us.
     const uint32_t pairs = nu_host ? nu_host * a.n_ff : kMaxU * a.n_ff;
     const uint32_t share = (pairs + grid - 1) / grid;
-    ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : 4;
+    ch = nu_host ? std::max<uint32_t>(1, (share + kProd - 1) / kProd) : std::max<uint32_t>(4, 2 * tpw);
 #if defined(Q4MI_TRACE) || defined(Q4MI_KNOBS)
     if (getenv("Q4MI_CHUNK")) ch = std::max(1, atoi(getenv("Q4MI_CHUNK")));
 #endif
@@ -1242,11 +1246,12 @@ static size_t dn_plan(MoeArgs &a, uint32_t nu_host, size_t cap_bytes, uint32_t &
     const size_t fixed = head_bytes(ty) + (size_t)kMaxU * NT * a.dn_rows * 4 +
                          al16((size_t)cap * a.n_ff + (size_t)cap * (a.n_ff / 32) * 4);
     // host lists: one chunk per producer; device lists (up to kMaxU experts)
-    // 3 experts, so a window's chunks land one after another and the items
+    // 2 experts, so a window's chunks land one after another and the items
     // start before the last (4-token window: 2 / 3 / 4 / 16 experts per chunk
-    // 33.5 / 33.6 / 33.7 / 34.8 us with 8-pair gate/up chunks)
+    // 33.5 / 33.6 / 33.7 / 34.8 us with 8-pair gate/up chunks; at hidden 2560
+    // with IQ4_NL down, 2 / 3 / 5: 21.2 / 21.8 / 23.3 us)
     const uint32_t nu_est = nu_host ? nu_host : kMaxU;
-    ch = nu_host ? std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd) : 3;
+    ch = nu_host ? std::max<uint32_t>(1, (nu_est + kProd - 1) / kProd) : 2;
 #if defined(Q4MI_TRACE) || defined(Q4MI_KNOBS)
     if (getenv("Q4MI_DNCHUNK")) ch = std::max(1, atoi(getenv("Q4MI_DNCHUNK")));
 #endif
@@ -1268,7 +1273,7 @@ template <uint32_t TY, int NT, int TPR, int GPT>
 static bool launch_gu(MoeArgs a, uint32_t nu_host) {
     const uint32_t grid = (uint32_t)cu_count();
     uint32_t ch, S;
-    const size_t lds = gu_plan<NT>(a, nu_host, grid, lds_cap(), ch, S, TY);
+    const size_t lds = gu_plan<NT>(a, nu_host, grid, lds_cap(), ch, S, TY, 64u / TPR);
     if (!lds) {
         set_error("moe_gu_k: LDS limit");
         return false;
