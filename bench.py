@@ -783,9 +783,11 @@ def bench_prefill_xg(L, torch, np, q4mi, synth, args, copies=3, reps=10):
 
 def bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, timed, args):
     """configs[1] with its router in front (the f1/f2 row): per layer
-    q4mi_moe_route (fp32 512 x 2048 router GEMV, the shared expert's sigmoid
-    gate, softmax top-10 into the device list with the shared expert at
-    weight sg) then q4_hip_moe_exec_dev, sustained over the layer stack.
+    q4mi_moe_route_exec (fp32 512 x 2048 router GEMV and the shared expert's
+    sigmoid gate, then the device-list decode layer whose gate/up blocks take
+    the softmax top-10 themselves, the shared expert at weight sg; the lists
+    are written as q4mi_moe_route writes them), sustained over the layer
+    stack.
     Bytes per layer add the 4 MB router and the 8 KB gate vector."""
     P = q4mi.ptr
     T = q4mi.T_IQ3_S
@@ -802,13 +804,11 @@ def bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, ti
 
     def stack():
         for l in range(NL):
-            q4mi.check(L.q4mi_moe_route(P(routers[l]), 0, P(sgate[l]), P(xs[l]), 1, N_EMBD, N_EXP,
-                                        TOPK, P(lg[l]), P(es[l]), P(ew[l]), P(nh[l]), 64, N_EXP,
-                                        P(sg[l])), "q4mi_moe_route")
-            q4mi.check(L.q4_hip_moe_exec_dev(arenas[l].data_ptr(), stride, P(es[l]), P(ew[l]),
-                                             P(nh[l]), T, og, T, ou, T, od, P(xs[l]), None, None,
-                                             None, P(ys[l]), N_FF, N_EMBD, N_EMBD),
-                       "q4_hip_moe_exec_dev")
+            q4mi.check(L.q4mi_moe_route_exec(P(routers[l]), 0, P(sgate[l]), P(xs[l]), N_EMBD,
+                                             N_EXP, TOPK, P(lg[l]), P(es[l]), P(ew[l]), P(nh[l]),
+                                             N_EXP, P(sg[l]), arenas[l].data_ptr(), stride, T,
+                                             og, T, ou, T, od, P(ys[l]), N_FF),
+                       "q4mi_moe_route_exec")
     gr = capture(stack)
     steps = max(args.steps // 4, 10)
     ms = timed(gr, steps, max(args.warmup // 4, 2))
@@ -819,8 +819,9 @@ def bench_routed(L, torch, np, q4mi, arenas, stride, og, ou, od, NL, capture, ti
             "GB/s": round(nbytes / t / 1e9, 1),
             "pct_of_hbm": round(100 * nbytes / t / 1e9 / HBM_PEAK, 2),
             "bytes_per_layer": nbytes,
-            "note": "router GEMV (fp32 512x2048) + sigmoid shared gate + top-10 into device "
-                    "lists, then the device-list decode layer; graph over the %d-layer stack"
+            "note": "router GEMV (fp32 512x2048) + sigmoid shared gate, then the device-list "
+                    "decode layer taking the top-10 in its gate/up blocks (3 launches); graph "
+                    "over the %d-layer stack"
                     % NL}
 
 

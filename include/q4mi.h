@@ -219,6 +219,22 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
                     uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
                     float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
                     uint32_t ostride, int32_t shared_slot, float *d_sg);
+/* One token's routed decode layer in three launches: q4mi_moe_route's
+ * router GEMV (d_logits, and d_sg with a gate vector), then the device-list
+ * decode layer of q4_hip_moe_exec_dev whose gate/up blocks take the top-k of
+ * d_logits themselves (the same code as q4mi_moe_route's top-k launch, so
+ * the same picks and weights bit for bit) instead of a fourth launch.  The
+ * lists are still written, with ostride 64 (d_ids, d_wts, d_nh: all three or
+ * none).  Arguments as q4mi_moe_route (n_tok 1) and q4_hip_moe_exec_dev
+ * (in_dim = n_embd); topk + (shared_slot >= 0) <= 64.  No reference
+ * counterpart: it fuses the route_dev_n_k launch of q4_moe_gpu_dev
+ * (src/q4_moe.c:2439) into the layer. */
+bool q4mi_moe_route_exec(const void *d_wr, uint32_t wr_type, const float *d_sgw,
+                         const float *d_x, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                         float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
+                         int32_t shared_slot, float *d_sg, const uint8_t *base, uint64_t stride,
+                         uint32_t gt, uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt,
+                         uint64_t od, float *d_y, uint32_t n_ff);
 /* d_y[t] += sigmoid(d_w . d_x[t]) * d_sh[t], t < n_tok: the shared
  * expert's gate applied to its separately computed output, one launch.
  * Replaces q4_hip_sgate_axpy (src/q4.h:1129-1131, src/q4_rocm.cu:15775-15800;

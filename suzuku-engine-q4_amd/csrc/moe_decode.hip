@@ -79,7 +79,8 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
                     const HostList &hl, uint32_t nu_host, uint32_t gt, uint64_t og, uint32_t ut,
                     uint64_t ou, uint32_t dt, uint64_t od, const float *d_x, float *d_y,
                     uint32_t n_ff, uint32_t in_dim, uint32_t n_embd, Work work = Work{},
-                    uint64_t stride_d = 0) {
+                    uint64_t stride_d = 0, bool (*pre)(void *) = nullptr,
+                    void *pre_arg = nullptr) {
     if (!base || !d_x || !d_y || src.n_tok < 1 || src.n_tok > kMaxT) {
         set_error("moe: bad arguments");
         return false;
@@ -103,6 +104,7 @@ static bool moe_run(const uint8_t *base, uint64_t stride, const ListSrc &src,
         return false;
     }
     if (!work.h && !moe_warm(n_ff)) return false;
+    if (pre && !pre(pre_arg)) return false;   // a launch the layer depends on
     MoeArgs a = {};
     a.base = base;
     a.stride = stride;
@@ -381,6 +383,59 @@ bool q4_hip_moe_exec_dev(const uint8_t *base, uint64_t stride, const int32_t *d_
     ListSrc src = {d_es, d_ew, d_nhit, kMaxU, 1, 0, 0};
     return moe_run(base, stride, src, hl, 0, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, in_dim,
                    n_embd);
+}
+
+/* One token's routed layer in three launches (see include/q4mi.h). */
+bool q4mi_moe_route_exec(const void *d_wr, uint32_t wr_type, const float *d_sgw,
+                         const float *d_x, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                         float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
+                         int32_t shared_slot, float *d_sg, const uint8_t *base, uint64_t stride,
+                         uint32_t gt, uint64_t og, uint32_t ut, uint64_t ou, uint32_t dt,
+                         uint64_t od, float *d_y, uint32_t n_ff) {
+    const bool lists = d_ids || d_wts || d_nh;
+    if (lists && !(d_ids && d_wts && d_nh)) {
+        set_error("q4mi_moe_route_exec: d_ids, d_wts and d_nh together or none");
+        return false;
+    }
+    if (topk + (shared_slot >= 0 ? 1u : 0u) > kMaxU) {
+        set_error("q4mi_moe_route_exec: more than %u entries", kMaxU);
+        return false;
+    }
+    if (!router_front(d_wr, wr_type, d_sgw, d_x, 1, n_embd, n_exp, topk, d_logits, kMaxU,
+                      shared_slot, d_sg, false))
+        return false;
+    if (!(g_phases & 1)) {   // the down launch reads the plan gate/up built
+        set_error("q4mi_moe_route_exec: needs the gate/up launch (measurement phases)");
+        return false;
+    }
+    ListSrc src = {};
+    src.n_tok = 1;
+    src.stride = kMaxU;
+    src.lg = d_logits;
+    src.sg = d_sgw ? d_sg : nullptr;
+    src.o_ids = d_ids;
+    src.o_wts = d_wts;
+    src.o_nh = d_nh;
+    src.n_exp = n_exp;
+    src.topk = topk;
+    src.shared = shared_slot;
+    struct Front {
+        const void *wr;
+        uint32_t ty;
+        const float *sgw, *x;
+        uint32_t n_embd, n_exp, topk;
+        float *lg;
+        int32_t shared;
+        float *sg;
+    } f = {d_wr, wr_type, d_sgw, d_x, n_embd, n_exp, topk, d_logits, shared_slot, d_sg};
+    auto launch = [](void *p) {
+        const Front &g = *(const Front *)p;
+        return router_front(g.wr, g.ty, g.sgw, g.x, 1, g.n_embd, g.n_exp, g.topk, g.lg, kMaxU,
+                            g.shared, g.sg, true);
+    };
+    HostList hl = {};
+    return moe_run(base, stride, src, hl, 0, gt, og, ut, ou, dt, od, d_x, d_y, n_ff, n_embd,
+                   n_embd, Work{}, 0, launch, &f);
 }
 
 /* Window coverage: 2..8 tokens, gate type == up type, IQ3_S or Q8_0 with a

@@ -46,6 +46,7 @@
 
 #include "formats.h"
 #include "mmvq_engine.h"
+#include "route_wave.h"
 #include "q4mi_internal.h"
 
 namespace q4mi {
@@ -82,6 +83,17 @@ struct ListSrc {
     uint32_t n_tok;
     uint32_t n_fixed;    // count per token when nh is null / host list length
     uint32_t unique;     // host list already deduplicated (one token)
+    // One token's router logits in place of the lists (lg non-null): the
+    // plan's entries are route_k's top-k of lg [n_exp] plus, with shared >= 0,
+    // expert `shared` at weight sg[0] (or 1); gate/up block 0 writes them to
+    // o_ids / o_wts / o_nh (row 0, topk + 1 entries) as route_k would.
+    const float *lg;
+    const float *sg;
+    int32_t *o_ids;
+    float *o_wts;
+    int32_t *o_nh;
+    uint32_t n_exp, topk;
+    int32_t shared;
 };
 
 struct __align__(16) Plan {
@@ -97,50 +109,83 @@ struct __align__(16) Plan {
 
 // Device lists: wave 0 builds the plan (first-appearance order over
 // (token, pick)); callers sync afterwards.
+// LG: the source holds one token's router logits (ListSrc::lg) instead of
+// the lists; a separate instantiation, so that the other kernels do not
+// carry the top-k code (their start-up runs with a cold instruction cache).
+template <bool LG>
 __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *ht) {
-    // lane -> (token, pick) of the flattened lists, token-major
-    // every token's count in one load (lane t holds token t's), then
-    // read back lane by lane: one memory round trip, not one per token
-    const int cnt_l = lane < s.n_tok ? (s.nh ? s.nh[lane] : (int)s.n_fixed) : 0;
-    // the entries are loaded in the same round trip as the counts, assuming
-    // each token has at most CAP = 64 / (n_tok rounded up to a power of two)
-    // of them (lane l: token l / CAP, entry l % CAP; within the lists' rows);
-    // a longer list loads them again once the counts are known
-    const uint32_t cap_sh = s.n_tok <= 1 ? 6u : s.n_tok == 2 ? 5u : s.n_tok <= 4 ? 4u : 3u;
-    const uint32_t st = lane >> cap_sh, sr = lane & ((1u << cap_sh) - 1u);
-    int32_t sid = -1;
-    float sw = 0.f;
-    if (st < s.n_tok && sr < s.stride) {
-        sid = s.es[(size_t)st * s.stride + sr];
-        sw = s.ew[(size_t)st * s.stride + sr];
-    }
-    uint32_t E = 0, tok = 0, rem = 0;
-    bool found = false;
-    for (uint32_t t = 0; t < s.n_tok; t++) {
-        int c = __builtin_amdgcn_readlane(cnt_l, t);
-        if (c < 0) c = 0;
-        if ((uint32_t)c > s.stride) c = (int)s.stride;
-        if (!found && lane < E + (uint32_t)c) {
-            found = true;
-            tok = t;
-            rem = lane - E;
-        }
-        E += (uint32_t)c;
-    }
-    if (E > kMaxU) E = kMaxU;
+    uint32_t E = 0, tok = 0;
     int32_t id = -1;
     float w = 0.f;
-    if (__ballot(lane < E && rem >= (1u << cap_sh)) == 0) {
-        const int src = (int)((tok << cap_sh) + rem);
-        const int32_t gid = __shfl(sid, src);
-        const float gw = __shfl(sw, src);
-        if (lane < E) {
-            id = gid;
-            w = gw;
+    if constexpr (LG) {
+        // one token's router logits: route_k's top-k (same code, same
+        // picks and weights) and the shared entry after them; gate/up block
+        // 0 also writes them out as route_k's lists
+        int32_t *s_id = (int32_t *)(ht + 1024);
+        float *s_p = (float *)(ht + 1024 + 64);
+        const uint32_t tk = route_wave<8>(s.lg, s.n_exp, s.topk, lane, s_id, s_p);
+        float sk = 0.f;
+        for (uint32_t k = 0; k < tk; k++) sk += s_p[k];
+        const float inv2 = sk > 0.f ? __fdiv_rn(1.f, sk) : 0.f;
+        const uint32_t nsh = s.shared >= 0 ? 1u : 0u;
+        E = s.topk + nsh;
+        if (lane < s.topk) {
+            id = lane < tk ? s_id[lane] : -1;
+            w = lane < tk ? (sk > 0.f ? s_p[lane] * inv2 : s_p[lane]) : 0.f;
+        } else if (lane == s.topk && nsh) {
+            id = s.shared;
+            w = s.sg ? s.sg[0] : 1.f;
         }
-    } else if (lane < E) {
-        id = s.es[(size_t)tok * s.stride + rem];
-        w = s.ew[(size_t)tok * s.stride + rem];
+        if (s.o_ids && blockIdx.x == 0) {
+            if (lane < E) {
+                s.o_ids[lane] = id;
+                s.o_wts[lane] = w;
+            }
+            if (lane == 0 && s.o_nh) s.o_nh[0] = (int32_t)E;
+        }
+    } else {
+        // lane -> (token, pick) of the flattened lists, token-major
+        // every token's count in one load (lane t holds token t's), then
+        // read back lane by lane: one memory round trip, not one per token
+        const int cnt_l = lane < s.n_tok ? (s.nh ? s.nh[lane] : (int)s.n_fixed) : 0;
+        // the entries are loaded in the same round trip as the counts, assuming
+        // each token has at most CAP = 64 / (n_tok rounded up to a power of two)
+        // of them (lane l: token l / CAP, entry l % CAP; within the lists' rows);
+        // a longer list loads them again once the counts are known
+        const uint32_t cap_sh = s.n_tok <= 1 ? 6u : s.n_tok == 2 ? 5u : s.n_tok <= 4 ? 4u : 3u;
+        const uint32_t st = lane >> cap_sh, sr = lane & ((1u << cap_sh) - 1u);
+        int32_t sid = -1;
+        float sw = 0.f;
+        if (st < s.n_tok && sr < s.stride) {
+            sid = s.es[(size_t)st * s.stride + sr];
+            sw = s.ew[(size_t)st * s.stride + sr];
+        }
+        uint32_t rem = 0;
+        bool found = false;
+        for (uint32_t t = 0; t < s.n_tok; t++) {
+            int c = __builtin_amdgcn_readlane(cnt_l, t);
+            if (c < 0) c = 0;
+            if ((uint32_t)c > s.stride) c = (int)s.stride;
+            if (!found && lane < E + (uint32_t)c) {
+                found = true;
+                tok = t;
+                rem = lane - E;
+            }
+            E += (uint32_t)c;
+        }
+        if (E > kMaxU) E = kMaxU;
+        if (__ballot(lane < E && rem >= (1u << cap_sh)) == 0) {
+            const int src = (int)((tok << cap_sh) + rem);
+            const int32_t gid = __shfl(sid, src);
+            const float gw = __shfl(sw, src);
+            if (lane < E) {
+                id = gid;
+                w = gw;
+            }
+        } else if (lane < E) {
+            id = s.es[(size_t)tok * s.stride + rem];
+            w = s.ew[(size_t)tok * s.stride + rem];
+        }
     }
     const bool valid = lane < E && id >= 0;
     // First occurrence of each id, through a 1024-bucket table in LDS (ht,
@@ -839,7 +884,7 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     }
 }
 
-template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
+template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT, bool LG>
 __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t bid = blockIdx.x, nblk = gridDim.x, ch = a.chunk, S = a.slots;
@@ -876,7 +921,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
             if (c0 + k * kCons < nq) v0[k] = ((const float4 *)a.x)[c0 + k * kCons];
     }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) build_plan(P, a.src, tid, (uint32_t *)ring);
+    if (!uniq && tid < 64) build_plan<LG>(P, a.src, tid, (uint32_t *)ring);
     Q4MI_TR(13, 0, tid == 0);
     Q4MI_TR(14, 0, tid == kProd * 64);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -1161,7 +1206,7 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
             for (uint32_t i = tid; i < sizeof(Plan) / 16; i += 64)
                 ((uint4 *)P)[i] = ((const uint4 *)a.gplan)[i];
         } else {
-            build_plan(P, a.src, tid, (uint32_t *)ring);
+            build_plan<false>(P, a.src, tid, (uint32_t *)ring);
         }
     }
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -1190,8 +1235,9 @@ constexpr size_t kLdsCap = 160 * 1024;
 // moe_decode.hip).
 size_t lds_cap();
 
-// bytes of the bucket table build_plan keeps at the start of the ring
-constexpr size_t kPlanTable = 4096;
+// bytes build_plan uses at the start of the ring: its 1024-bucket table,
+// then (router logits) one token's 64 picks and probabilities
+constexpr size_t kPlanTable = 4096 + 512;
 
 static size_t head_bytes(uint32_t ty) {
     const size_t tab = ty == Q4MI_T_IQ3_S   ? tab_bytes<Q4MI_T_IQ3_S>()
@@ -1281,17 +1327,24 @@ static bool launch_gu(MoeArgs a, uint32_t nu_host) {
     a.chunk = ch;
     a.slots = S;
     const bool wide = ((((uintptr_t)a.base) | a.stride | a.og | a.ou | a.rb_gu) & 15u) == 0;
-    const void *fn = wide ? (const void *)moe_gu_k<TY, NT, TPR, GPT, 16>
-                          : (const void *)moe_gu_k<TY, NT, TPR, GPT, 4>;
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-        set_error("moe_gu_k: LDS limit (%zu)", lds);
+    auto go = [&](auto kern) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) {
+            set_error("moe_gu_k: LDS limit (%zu)", lds);
+            return false;
+        }
+        kern<<<dim3(grid), dim3(kT), lds, stream()>>>(a);
+        return launch_ok("moe_gu_k");
+    };
+    if (a.src.lg) {   // router logits (one token)
+        if constexpr (NT == 1)
+            return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, true>)
+                        : go(moe_gu_k<TY, NT, TPR, GPT, 4, true>);
+        set_error("moe_gu_k: router logits take one token");
         return false;
     }
-    if (wide)
-        moe_gu_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
-    else
-        moe_gu_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
-    return launch_ok("moe_gu_k");
+    return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, false>)
+                : go(moe_gu_k<TY, NT, TPR, GPT, 4, false>);
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>

@@ -76,6 +76,12 @@ bool route_list_launch(const float *lg, int32_t *ids, float *wts, int32_t *nh, u
                        uint32_t n_exp, uint32_t topk, uint32_t ostride, int32_t shared,
                        const float *sg);
 
+// Router GEMV of q4mi_moe_route (router.hip); launch = false: checks only.
+bool router_front(const void *d_wr, uint32_t wr_type, const float *d_sgw, const float *d_x,
+                  uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                  float *d_logits, uint32_t ostride, int32_t shared_slot, float *d_sg,
+                  bool launch);
+
 // Compute units of the current device (persistent grids size to it).
 int cu_count();
 

@@ -157,18 +157,14 @@ __global__ void dot_sigmoid_k(const float *__restrict__ a, const float *__restri
     if (threadIdx.x == 0) *out = 1.f / (1.f + expf(-d));
 }
 
-}  // namespace q4mi
-
-using namespace q4mi;
-
-extern "C" {
-
-/* Router front of a MoE layer (see include/q4mi.h). */
-bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, const float *d_x,
-                    uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
-                    float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
-                    uint32_t ostride, int32_t shared_slot, float *d_sg) {
-    if (!d_wr || !d_x || !d_logits || !d_ids || !d_wts || !n_tok || !n_exp || n_exp > 512u ||
+// The router GEMV of q4mi_moe_route (logits [n_tok][n_exp] and, with a gate
+// vector, sg[t] = sigmoid(w_sg . x_t)); launch = false only checks the
+// arguments (the error text says which is wrong).
+bool router_front(const void *d_wr, uint32_t wr_type, const float *d_sgw, const float *d_x,
+                  uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                  float *d_logits, uint32_t ostride, int32_t shared_slot, float *d_sg,
+                  bool launch) {
+    if (!d_wr || !d_x || !d_logits || !n_tok || !n_exp || n_exp > 512u ||
         !topk || topk > 64u) {
         set_error("q4mi_moe_route: bad arguments");
         return false;
@@ -196,6 +192,7 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
         set_error("q4mi_moe_route: x, router and gate rows must be 16-byte aligned");
         return false;
     }
+    if (!launch) return true;
     const uint32_t TT = std::min<uint32_t>(std::min<uint32_t>(8u, 16384u / n_embd), n_tok);
     const uint32_t gy = (n_tok + TT - 1) / TT;
     const uint32_t rows = n_exp + (d_sgw ? 1u : 0u);
@@ -213,7 +210,29 @@ bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, cons
     else
         router_gemv_k<kRtBF16><<<grid, 256, lds, stream()>>>(w, d_sgw, d_x, n_tok, n_embd, n_exp,
                                                              TT, d_logits, d_sg);
-    if (!launch_ok("router_gemv_k")) return false;
+    return launch_ok("router_gemv_k");
+}
+
+}  // namespace q4mi
+
+using namespace q4mi;
+
+extern "C" {
+
+/* Router front of a MoE layer (see include/q4mi.h). */
+bool q4mi_moe_route(const void *d_wr, uint32_t wr_type, const float *d_sgw, const float *d_x,
+                    uint32_t n_tok, uint32_t n_embd, uint32_t n_exp, uint32_t topk,
+                    float *d_logits, int32_t *d_ids, float *d_wts, int32_t *d_nh,
+                    uint32_t ostride, int32_t shared_slot, float *d_sg) {
+    if (!d_ids || !d_wts) {
+        set_error("q4mi_moe_route: bad arguments");
+        return false;
+    }
+    if (!router_front(d_wr, wr_type, d_sgw, d_x, n_tok, n_embd, n_exp, topk, d_logits, ostride,
+                      shared_slot, d_sg, false) ||
+        !router_front(d_wr, wr_type, d_sgw, d_x, n_tok, n_embd, n_exp, topk, d_logits, ostride,
+                      shared_slot, d_sg, true))
+        return false;
     return route_list_launch(d_logits, d_ids, d_wts, d_nh, n_tok, n_exp, topk, ostride,
                              shared_slot, d_sgw ? d_sg : nullptr);
 }

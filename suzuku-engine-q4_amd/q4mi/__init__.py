@@ -74,6 +74,9 @@ _SIGS = {
     "q4_hip_softmax_topk": (_b, [_vp, _u32, _u32, _vp, _vp]),
     "q4mi_moe_route": (_b, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp,
                             _u32, _c.c_int32, _vp]),
+    "q4mi_moe_route_exec": (_b, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp,
+                                 _c.c_int32, _vp, _vp, _u64, _u32, _u64, _u32, _u64, _u32,
+                                 _u64, _vp, _u32]),
     "q4_hip_sgate_axpy": (_b, [_vp, _vp, _vp, _vp, _u32, _u32]),
     "q4_hip_dot_sigmoid": (_b, [_vp, _vp, _vp, _u32]),
     "q4mi_assign": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),

@@ -148,6 +148,77 @@ def test_routed_layer_with_gated_shared_expert(gpu, oracle, n_tok):
     assert rel_err(host(y), yo) <= TOL
 
 
+@pytest.mark.parametrize("gate,rtype,n_exp,topk", [(True, 0, 512, 10), (False, 30, 512, 10),
+                                                   (True, 1, 200, 63), (True, 0, 8, 10)])
+def test_route_exec_equals_route_then_exec_dev(gpu, oracle, gate, rtype, n_exp, topk):
+    """q4mi_moe_route_exec (top-k taken inside the layer's gate/up blocks)
+    against q4mi_moe_route + q4_hip_moe_exec_dev on the same inputs: logits,
+    gate, lists and y equal bit for bit (the same top-k code on the same
+    logits); and y against the oracle's layer with the oracle's routing.
+    Covers fewer experts than picks (n_exp 8 < topk 10: ids -1 past n_exp)
+    and 63 picks + the shared entry (the 64-entry bound)."""
+    import torch
+    from test_gpu_decode import layer
+    ly = layer()
+    H, F = ly.n_embd, ly.n_ff
+    rng = np.random.default_rng(90 + topk + n_exp)
+    w = router_rows(rng, rtype, n_exp, H)
+    g = (rng.standard_normal(H) * 0.02).astype(np.float32) if gate else None
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    dx, dw = dev(x), dev(w)
+    dg = dev(g) if gate else None
+    P = q4mi.ptr
+    shared = 512
+    outs = []
+    for fused in (False, True):
+        lg, ids, wts, nh = zeros((1, n_exp)), zeros((1, 64), torch.int32), zeros((1, 64)), \
+            zeros(1, torch.int32)
+        ids.fill_(-7)
+        sg, y = zeros(1), zeros((1, H))
+        gp = P(dg) if gate else None
+        if fused:
+            q4mi.check(gpu.q4mi_moe_route_exec(P(dw), rtype, gp, P(dx), H, n_exp, topk, P(lg),
+                                               P(ids), P(wts), P(nh), shared, P(sg),
+                                               P(ly.d_arena), ly.stride, T_IQ3_S, ly.og,
+                                               T_IQ3_S, ly.ou, T_IQ3_S, ly.od, P(y), F),
+                       "route_exec")
+        else:
+            q4mi.check(gpu.q4mi_moe_route(P(dw), rtype, gp, P(dx), 1, H, n_exp, topk, P(lg),
+                                          P(ids), P(wts), P(nh), 64, shared, P(sg)), "route")
+            q4mi.check(gpu.q4_hip_moe_exec_dev(P(ly.d_arena), ly.stride, P(ids), P(wts), P(nh),
+                                               T_IQ3_S, ly.og, T_IQ3_S, ly.ou, T_IQ3_S, ly.od,
+                                               P(dx), None, None, None, P(y), F, H, H),
+                       "exec_dev")
+        E = topk + 1
+        outs.append([host(t) for t in (lg, sg, y)] + [host(ids)[:, :E], host(wts)[:, :E],
+                                                      host(nh)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    oid, ow = oracle.softmax_topk(outs[1][0], min(topk, n_exp))
+    got = outs[1][3][0, :min(topk, n_exp)]
+    assert np.array_equal(got, oid[0])
+    sgv = outs[1][1][0] if gate else 1.0
+    sid = np.concatenate([oid, np.full((1, 1), shared, np.int32)], 1)
+    sw = np.concatenate([ow, np.full((1, 1), sgv, np.float32)], 1).astype(np.float32)
+    yo = oracle.moe_tokens(H, F, T_IQ3_S, T_IQ3_S, ly.arena, ly.stride, x, sid, sw)
+    assert rel_err(outs[1][2], yo) <= TOL
+
+
+def test_route_exec_rejects(gpu):
+    """Partial list outputs and more than 64 entries are refused before any
+    launch."""
+    import torch
+    P = q4mi.ptr
+    b = zeros(4096)
+    i = zeros(64, torch.int32)
+    assert not gpu.q4mi_moe_route_exec(P(b), 0, None, P(b), 256, 8, 10, P(b), P(i), None, None,
+                                       -1, None, P(b), 0, T_IQ3_S, 0, T_IQ3_S, 0, T_IQ3_S, 0,
+                                       P(b), 256)
+    assert not gpu.q4mi_moe_route_exec(P(b), 0, None, P(b), 256, 64, 64, P(b), None, None, None,
+                                       5, None, P(b), 0, T_IQ3_S, 0, T_IQ3_S, 0, T_IQ3_S, 0,
+                                       P(b), 256)
+
+
 def test_sgate_axpy_and_dot_sigmoid(gpu, oracle):
     """q4_hip_sgate_axpy / q4_hip_dot_sigmoid (the reference's separate gate
     application): sg equals the oracle's gate (the router's dot order) to
