@@ -66,6 +66,7 @@ constexpr uint32_t kConsW = kCons / 64;       // consumer waves
 constexpr uint32_t kDnRows = 8;       // output rows per down block (a call may take more)
 constexpr uint32_t kDnRowsMax = 16;   // ... up to this many, so the grid fits the CUs
 constexpr uint32_t kMaxS = 32;    // LDS ring slots
+constexpr int kSrcDev = 0, kSrcHost = 1, kSrcLogits = 2;   // list source of a launch
 // x quads per consumer thread loaded before the block barrier: all of a
 // window's, and a decode token's with the least prologue code (the prologue
 // runs with a cold instruction cache, on the critical path)
@@ -204,7 +205,7 @@ __device__ void build_plan(Plan *P, const ListSrc &s, uint32_t lane, uint32_t *h
     const uint32_t mlane = valid ? ht[hb] : lane;
     const bool clash = valid && __shfl(id, (int)mlane) != id;
     uint32_t first_j = (valid && !clash) ? mlane : lane;
-    if (__ballot(clash)) {
+    if (__builtin_expect(__ballot(clash) != 0, 0)) {
         first_j = lane;
         for (uint32_t j = 0; j < E; j++) {
             if (!((vmask >> j) & 1ull)) continue;
@@ -582,7 +583,7 @@ __device__ inline void note_timeout(uint32_t bit) { atomicOr(&g_moe_status, bit)
 __device__ inline void spin_ge(const uint32_t *p, uint32_t v) {
     uint32_t n = 0;
     for (; lds_ld(p) < v && n < kSpinMax; n++) __builtin_amdgcn_s_sleep(1);
-    if (n == kSpinMax) note_timeout(kStConsumer);
+    if (__builtin_expect(n == kSpinMax, 0)) note_timeout(kStConsumer);
     asm volatile("" ::: "memory");
 }
 __device__ inline void wait_chunk(const Sync *y, uint32_t c) {
@@ -647,7 +648,7 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
             idle++;
         }
     }
-    if (pub < C) note_timeout(kStProducer);
+    if (__builtin_expect(pub < C, 0)) note_timeout(kStProducer);
     wait_vm(0);
 }
 
@@ -747,7 +748,9 @@ __device__ inline void gu_quant_x(const MoeArgs &a, Sync *Y, int8_t *xq, float *
 #pragma unroll
     for (uint32_t k = 0; k < kXPre<NT>; k++)
         if (ct + k * kCons < nq) quant_quad(v0[k], ct + k * kCons, xq, xd);
-    // further quads (many tokens) four loads in flight at a time
+    // further quads (many tokens or a wide row) four loads in flight at a
+    // time; rare, so laid out after the common path
+    if (__builtin_expect(ct + kXPre<NT> * kCons < nq, 0))
     for (uint32_t i0 = ct + kXPre<NT> * kCons; i0 < nq; i0 += 4 * kCons) {
         float4 v[4];
 #pragma unroll
@@ -884,7 +887,11 @@ __device__ inline void gu_compute(const MoeArgs &a, const uint32_t *stab, const 
     }
 }
 
-template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT, bool LG>
+// SRC: kSrcDev device lists, kSrcHost a host list in the kernel arguments
+// (one token), kSrcLogits router logits (one token).  Separate
+// instantiations, so that each kernel carries only its own list code: the
+// start-up runs with a cold instruction cache, on the critical path.
+template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT, int SRC>
 __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t bid = blockIdx.x, nblk = gridDim.x, ch = a.chunk, S = a.slots;
@@ -900,7 +907,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const KArgs ka = kargs();
-    const bool uniq = a.src.unique != 0;
+    constexpr bool uniq = SRC == kSrcHost;
     // the host list's ids, loaded while the block starts up (lane u: id u)
     const int32_t hid = (uniq && wave < kProd) ? host_ids(ka, a.src.n_fixed) : -1;
     // consumers issue their prologue loads (codebook entry, first x quad)
@@ -921,7 +928,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
             if (c0 + k * kCons < nq) v0[k] = ((const float4 *)a.x)[c0 + k * kCons];
     }
     if (tid < sizeof(Sync) / 4) ((uint32_t *)Y)[tid] = 0;
-    if (!uniq && tid < 64) build_plan<LG>(P, a.src, tid, (uint32_t *)ring);
+    if (!uniq && tid < 64) build_plan<SRC == kSrcLogits>(P, a.src, tid, (uint32_t *)ring);
     Q4MI_TR(13, 0, tid == 0);
     Q4MI_TR(14, 0, tid == kProd * 64);
     __syncthreads();                 // the only block-wide barrier: Sync zeroed, plan built
@@ -1155,7 +1162,7 @@ __device__ inline float dn_y_early(const MoeArgs &a, uint32_t c0, uint32_t r0, u
     return 0.f;
 }
 
-template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT>
+template <uint32_t TY, int NT, int TPR, int GPT, uint32_t UNIT, int SRC>
 __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t bid = blockIdx.x, ch = a.chunk, S = a.slots;
@@ -1175,7 +1182,7 @@ __global__ __launch_bounds__(kT) void moe_dn_k(MoeArgs a) {
     const uint32_t r0 = bid * a.dn_rows;
     const uint32_t nr = min(a.dn_rows, a.n_embd - r0);
     const KArgs ka = kargs();
-    const bool uniq = a.src.unique != 0;
+    constexpr bool uniq = SRC == kSrcHost;
     // the host list's ids (producers) or weights (consumers), loaded while
     // the block starts up (lane u: entry u)
     const int32_t hword = !uniq ? 0 : wave < kProd ? host_ids(ka, a.src.n_fixed)
@@ -1336,15 +1343,19 @@ static bool launch_gu(MoeArgs a, uint32_t nu_host) {
         kern<<<dim3(grid), dim3(kT), lds, stream()>>>(a);
         return launch_ok("moe_gu_k");
     };
-    if (a.src.lg) {   // router logits (one token)
-        if constexpr (NT == 1)
-            return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, true>)
-                        : go(moe_gu_k<TY, NT, TPR, GPT, 4, true>);
-        set_error("moe_gu_k: router logits take one token");
+    if constexpr (NT == 1) {
+        if (a.src.lg)   // router logits
+            return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, kSrcLogits>)
+                        : go(moe_gu_k<TY, NT, TPR, GPT, 4, kSrcLogits>);
+        if (a.src.unique)   // host list
+            return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, kSrcHost>)
+                        : go(moe_gu_k<TY, NT, TPR, GPT, 4, kSrcHost>);
+    } else if (a.src.lg || a.src.unique) {
+        set_error("moe_gu_k: host lists and router logits take one token");
         return false;
     }
-    return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, false>)
-                : go(moe_gu_k<TY, NT, TPR, GPT, 4, false>);
+    return wide ? go(moe_gu_k<TY, NT, TPR, GPT, 16, kSrcDev>)
+                : go(moe_gu_k<TY, NT, TPR, GPT, 4, kSrcDev>);
 }
 
 template <uint32_t TY, int NT, int TPR, int GPT>
@@ -1367,18 +1378,26 @@ static bool launch_dn(MoeArgs a, uint32_t nu_host) {
     // units need that run (not each row) 16-byte aligned and sized
     const bool wide = ((((uintptr_t)a.base) | a.stride_d | a.od | ((uint64_t)a.dn_rows * a.rb_dn)) & 15u) == 0 &&
                       a.n_embd % a.dn_rows == 0;
-    const void *fn = wide ? (const void *)moe_dn_k<TY, NT, TPR, GPT, 16>
-                          : (const void *)moe_dn_k<TY, NT, TPR, GPT, 4>;
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-        set_error("moe_dn_k: LDS limit (%zu)", lds);
+    const uint32_t grid = (a.n_embd + a.dn_rows - 1) / a.dn_rows;
+    auto go = [&](auto kern) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) {
+            set_error("moe_dn_k: LDS limit (%zu)", lds);
+            return false;
+        }
+        kern<<<dim3(grid), dim3(kT), lds, stream()>>>(a);
+        return launch_ok("moe_dn_k");
+    };
+    if constexpr (NT == 1) {
+        if (a.src.unique)   // host list
+            return wide ? go(moe_dn_k<TY, NT, TPR, GPT, 16, kSrcHost>)
+                        : go(moe_dn_k<TY, NT, TPR, GPT, 4, kSrcHost>);
+    } else if (a.src.unique) {
+        set_error("moe_dn_k: host lists take one token");
         return false;
     }
-    const uint32_t grid = (a.n_embd + a.dn_rows - 1) / a.dn_rows;
-    if (wide)
-        moe_dn_k<TY, NT, TPR, GPT, 16><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
-    else
-        moe_dn_k<TY, NT, TPR, GPT, 4><<<dim3(grid), dim3(kT), lds, stream()>>>(a);
-    return launch_ok("moe_dn_k");
+    return wide ? go(moe_dn_k<TY, NT, TPR, GPT, 16, kSrcDev>)
+                : go(moe_dn_k<TY, NT, TPR, GPT, 4, kSrcDev>);
 }
 
 // Gate/up lanes per pair: 32 (two or more groups per lane, two pairs per
