@@ -58,16 +58,19 @@ __global__ __launch_bounds__(NTHR) void mmvq_k(const uint8_t *__restrict__ W, ui
     if constexpr (!XF) load_xregs<NT, GPT, TPR>(x, xq, xd, K, nt, gi);
     if constexpr (XF) {
         // 8 lanes per 32-value group, nh / 8 groups per pass; the loads of
-        // up to 8 passes are issued before any is used (a load issued
-        // behind the tile copies returns only when they have landed, so one
-        // wait must cover all of them)
+        // kB passes are issued before any is used (a load issued behind the
+        // tile copies returns only when they have landed, so one wait must
+        // cover all of them)
         int8_t *lq = (int8_t *)(tile + ((R * rb + 15u) & ~15u));
         float *ld = (float *)(lq + (size_t)NT * K);
+        // kB passes per round: one round covers a short x at any block size
+        // (a larger kB is start-up code that such a call skips)
+        constexpr int kB = NTHR >= 1024 ? 2 : NTHR >= 512 ? 4 : 8;
         const uint32_t ng = nt * G, step = nh / 8, sub = hid & 7u;
-        for (uint32_t g0 = hid >> 3; g0 < ng; g0 += 8 * step) {
-            float4 v[8];
+        for (uint32_t g0 = hid >> 3; g0 < ng; g0 += kB * step) {
+            float4 v[kB];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 0; k < kB; k++) {
                 const uint32_t gid = g0 + k * step;
                 if (gid < ng) {
                     const uint32_t t = gid / G, g = gid % G;
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(NTHR) void mmvq_k(const uint8_t *__restrict__ W, ui
                 }
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 0; k < kB; k++) {
                 const uint32_t gid = g0 + k * step;
                 if (gid < ng) {   // uniform per 8-lane team
                     const uint32_t t = gid / G, g = gid % G;

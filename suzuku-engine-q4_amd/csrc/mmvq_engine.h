@@ -221,7 +221,8 @@ __device__ inline void lds_dma16(const void *g, uint32_t lds) {
 __device__ inline void stage_tile_issue(uint8_t *dst, const uint8_t *src, uint32_t nbytes,
                                         uint32_t tid, uint32_t nthr) {
     const uintptr_t a = (uintptr_t)src | nbytes;
-    if ((a & 15u) == 0) {
+    // (the register-copy fallbacks are laid out after the common path)
+    if (__builtin_expect((a & 15u) == 0, 1)) {
         // every copy of the block in flight at once (1 KB per wave op)
         const uint32_t lane = tid & 63u, nw = nthr / 64;
         const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);

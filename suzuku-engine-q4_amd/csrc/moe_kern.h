@@ -621,6 +621,9 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
 #ifdef Q4MI_TRACE
     Q4MI_TR(17, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
 #endif
+#if !defined(Q4MI_TRACE) && !defined(Q4MI_KNOBS)
+    ahead = 1;   // the product's setting, as a constant (one chunk in flight)
+#endif
     while (pub < C && idle < kSpinMax) {
         while (next < C && (next < pub + kProd * ahead) && slot_free(next)) {
             if (next >= S) lds_st(&y->cons[next % S], 0);
@@ -636,7 +639,11 @@ __device__ inline void produce(Sync *y, uint32_t *ends, uint32_t p, uint32_t C, 
         if (nloop++ == 0) Q4MI_TR(20, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
 #endif
         if (pub < next) {
+#if !defined(Q4MI_TRACE) && !defined(Q4MI_KNOBS)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // its only chunk in flight
+#else
             wait_vm(issued - ends[(pub / kProd) % kMaxS]);
+#endif
             lds_st(&y->landed[p], pub / kProd + 1);
 #ifdef Q4MI_TRACE
             if (npub < 4) Q4MI_TR(21 + npub, q4kern, p == 0 && (threadIdx.x & 63u) == 0);
@@ -670,9 +677,12 @@ __device__ inline void build_tables(uint8_t *smem, uint32_t code, uint32_t ct) {
 // LDS: [stab 32 KB] (IQ3_S) Plan Sync | xq [NT][K] | xd [NT][K/32] | ring of
 //      S slots, slot = gate rows[ch] then up rows[ch].
 //
-// Block `bid` of `nblk` takes pairs [PT*bid/nblk, PT*(bid+1)/nblk).
+// Block `bid` of `nblk` takes pairs [share_lo(bid), share_lo(bid + 1)).
 __device__ inline uint32_t share_lo(uint32_t PT, uint32_t bid, uint32_t nblk) {
-    return (uint32_t)(((uint64_t)PT * bid) / nblk);
+    // the first PT % nblk blocks take one pair more (one 32-bit division:
+    // a 64-bit one is ~100 scalar instructions of start-up code)
+    const uint32_t q = PT / nblk, r = PT % nblk;
+    return bid * q + min(bid, r);
 }
 
 // First pair of block `bid` when the blocks split the pairs by work: a pair
@@ -1046,7 +1056,9 @@ __device__ inline void dn_compute(const MoeArgs &a, const uint32_t *stab, Plan *
         if (ct + kCons < nq) quant_quad(v1, ct + kCons, hq, hd);
         i0 = ct + 2 * kCons;
     }
-    // further quads eight loads in flight at a time
+    // further quads eight loads in flight at a time (with the prologue's
+    // quads, only for many or long rows: laid out after the common path)
+    if (__builtin_expect(i0 < nq, !pre))
     for (; i0 < nq; i0 += 8 * kCons) {
         float4 v[8];
 #pragma unroll
