@@ -690,23 +690,28 @@ __device__ inline uint32_t share_lo(uint32_t PT, uint32_t bid, uint32_t nblk) {
 // gate and up rows shared by all of them, one dot per token -- so the
 // blocks holding an expert every token picked (the shared expert) get fewer
 // pairs.  Every wave computes the same value (lane u: expert u).
-__device__ inline uint32_t share_weighted(const Plan *P, uint32_t nu, uint32_t n_ff,
-                                          uint32_t bid, uint32_t nblk, uint32_t lane) {
+__device__ inline void share_weighted(const Plan *P, uint32_t nu, uint32_t n_ff, uint32_t bid,
+                                      uint32_t nblk, uint32_t lane, uint32_t &p0,
+                                      uint32_t &p1) {
     const uint32_t c = lane < nu ? 2u + (uint32_t)__popc(P->sel[lane]) : 0u;
     const uint32_t incl = q4mi_wave_incl_scan(c);
     const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-    if (bid >= nblk) return nu * n_ff;
-    // target in units of 1/n_ff of an expert's cost: t = total * n_ff * bid /
-    // nblk (< 2^32: total <= 64 * 10, n_ff <= 1024, bid < 4096)
-    const uint32_t t = total * n_ff * bid / nblk;
-    // expert u0 = number of experts whose whole cost ends at or before t
-    const uint64_t done = __ballot(incl * n_ff <= t && lane < nu);
-    const uint32_t u0 = (uint32_t)__popcll(done);
-    if (u0 >= nu) return nu * n_ff;
-    const uint32_t ex = (uint32_t)__builtin_amdgcn_readlane((int)(incl - c), (int)u0);
-    const uint32_t cu = (uint32_t)__builtin_amdgcn_readlane((int)c, (int)u0);
-    const uint32_t into = (t - ex * n_ff) / cu;   // pairs of u0 before t
-    return u0 * n_ff + min(into, n_ff);
+    auto at = [&](uint32_t b) -> uint32_t {
+        if (b >= nblk) return nu * n_ff;
+        // target in units of 1/n_ff of an expert's cost: t = total * n_ff * b /
+        // nblk (< 2^32: total <= 64 * 10, n_ff <= 1024, b < 4096)
+        const uint32_t t = total * n_ff * b / nblk;
+        // expert u0 = number of experts whose whole cost ends at or before t
+        const uint64_t done = __ballot(incl * n_ff <= t && lane < nu);
+        const uint32_t u0 = (uint32_t)__popcll(done);
+        if (u0 >= nu) return nu * n_ff;
+        const uint32_t ex = (uint32_t)__builtin_amdgcn_readlane((int)(incl - c), (int)u0);
+        const uint32_t cu = (uint32_t)__builtin_amdgcn_readlane((int)c, (int)u0);
+        const uint32_t into = (t - ex * n_ff) / cu;   // pairs of u0 before t
+        return u0 * n_ff + min(into, n_ff);
+    };
+    p0 = at(bid);
+    p1 = at(bid + 1);
 }
 
 // Producer: issue pairs [p0, p1) of the block (gate rows then up rows per
@@ -954,8 +959,7 @@ __global__ __launch_bounds__(kT) void moe_gu_k(MoeArgs a) {
         p0 = share_lo(PT, bid, nblk);
         p1 = share_lo(PT, bid + 1, nblk);
     } else {   // shares of equal work: an expert picked by more tokens costs more
-        p0 = share_weighted(P, nu, a.n_ff, bid, nblk, lane);
-        p1 = share_weighted(P, nu, a.n_ff, bid + 1, nblk, lane);
+        share_weighted(P, nu, a.n_ff, bid, nblk, lane, p0, p1);
     }
 
     if (wave < kProd) {
